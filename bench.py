@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""bench.py -- the RT4 quantized-matmul hot path on one MI355X.
+
+Workload (the configuration the metric is quoted on):
+one decode MLP step at the MTP3 verify width M=4 on 27B layer shapes, i.e. the
+three linears of one layer through the drop-in k_gemv_w4a8 entry (activation
+quantize + W4A8 GEMV each): gate and up (K=5120, N=17408) and down (K=17408,
+N=5120).  Consecutive steps walk through `--layers` distinct layers of random
+RT4 weights (1.1 GB at the default 8), as the runtime walks its layers, so
+weights stream from HBM rather than from the 256 MB MALL.  Inputs are resident
+in HBM before timing; steps are replayed from a HIP graph (no host launch
+overhead inside the timed region).
+
+value = algorithmic bytes of a step / time per step (GB/s), where the bytes of
+one linear are weights + fp16 scales + int8 activations + activation scales +
+fp32 output (46,257,408 B for gate/up, 46,113,024 B for down).
+
+Also printed in the same JSON line:
+  roofline      the dominant kernel (the gate/up GEMV launch), timed live with
+                HIP events over a graph of back-to-back launches
+  kernels       the same figure for the other kernels of the path
+  cpu_baseline  the reference's CPU path (numpy RT4 dequant + matmul, restated
+                in oracle/np_ref.py) on a bounded sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "k100lc-rt4_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X published HBM3E bandwidth
+I8_PEAK_TOPS = 5000.0          # MI355X published dense int8 MFMA
+
+
+def linear_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic HBM bytes of one W4A8 GEMV call."""
+    NG = K // 128
+    return N * K // 2 + N * NG * 2 + M * K + 2 * M * NG * 4 + M * N * 4
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=8, help="distinct weight sets rotated through")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the per-kernel table beyond the roofline")
+    return ap.parse_args()
+
+
+def timed_graph(torch, fn, reps: int = 5) -> float:
+    """Capture fn() in a HIP graph, replay it, return ms per replay (median of reps)."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    return statistics.median(times)
+
+
+def cpu_info() -> dict:
+    model = platform.processor()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu": model, "os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_baseline(step_bytes: int, seconds: float) -> dict:
+    """The reference's CPU path for one decode MLP step, parallel over output rows."""
+    import concurrent.futures as cf
+
+    import numpy as np
+    import threadpoolctl
+
+    from oracle import np_ref
+
+    rng = np.random.default_rng(0)
+    M = 4
+    shapes = [(17408, 5120), (17408, 5120), (5120, 17408)]
+    mats = []
+    for N, K in shapes:
+        wq = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint32).view(np.uint8).reshape(N, K // 2)
+        ws = (np.abs(rng.standard_normal((N, K // 128))) * 0.01 + 1e-3).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+        mats.append((wq, ws, np_ref.fake_quant_act(x)))
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+
+    def linear(pool, wq, ws, xf):
+        N = wq.shape[0]
+        bounds = np.linspace(0, N, threads + 1).astype(int)
+        futs = [pool.submit(np_ref.cpu_linear, wq[a:b], ws[a:b], xf) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
+        return np.concatenate([f.result() for f in futs], axis=1)
+
+    times = []
+    t_start = time.perf_counter()
+    with threadpoolctl.threadpool_limits(1), cf.ThreadPoolExecutor(threads) as pool:
+        while True:
+            t0 = time.perf_counter()
+            for wq, ws, xf in mats:
+                linear(pool, wq, ws, xf)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > seconds or len(times) >= 20:
+                break
+    med = statistics.median(times)
+    try:
+        blas = np.show_config(mode="dicts")["Build Dependencies"]["blas"]["name"]
+    except Exception:  # noqa: BLE001
+        blas = "unknown"
+    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(med * 1e3, 2),
+            "sample": f"{len(times)} decode MLP steps (gate+up+down, M=4, 27B shapes), numpy RT4 dequant + "
+                      f"matmul split over {threads} threads (1 BLAS thread each), median step",
+            "blas": blas, **cpu_info()}
+
+
+def main() -> int:
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (--gpus 1); multi-GPU scaling is not part "
+              "of it (the path would shard weight rows across GPUs with no exchange).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import rt4_amd
+    from rt4_amd import workload
+
+    metric = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+    torch.cuda.set_device(0)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    M = 4
+    (Ngu, Kgu), (Nd, Kd) = (17408, 5120), (5120, 17408)
+    L = max(1, args.layers)
+    layers = []
+    for _ in range(L):
+        layers.append({k: workload.weights_torch(N, K, generator=gen)
+                       for k, (N, K) in (("gate", (Ngu, Kgu)), ("up", (Ngu, Kgu)), ("down", (Nd, Kd)))})
+    x_gu = workload.acts_torch(M, Kgu, generator=gen)
+    x_d = workload.acts_torch(M, Kd, generator=gen)
+    y_g = torch.empty((M, Ngu), device="cuda")
+    y_u = torch.empty((M, Ngu), device="cuda")
+    y_d = torch.empty((M, Nd), device="cuda")
+
+    def step(i):
+        lw = layers[i % L]
+        rt4_amd.gemv_w4a8(*lw["gate"], x_gu, out=y_g)
+        rt4_amd.gemv_w4a8(*lw["up"], x_gu, out=y_u)
+        rt4_amd.gemv_w4a8(*lw["down"], x_d, out=y_d)
+
+    for i in range(L):                 # eager pass: grows scratch, sets kernel attributes
+        step(i)
+    torch.cuda.synchronize()
+
+    K_steps, W_steps = max(1, args.steps), max(0, args.warmup)
+    g_timed = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_timed):
+        for i in range(K_steps):
+            step(i)
+    if W_steps:
+        g_warm = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_warm):
+            for i in range(W_steps):
+                step(i)
+        g_warm.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    g_timed.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / K_steps
+    # the last timed step used layer (K-1) % L; the replay must reproduce the eager result
+    graph_out = y_d.clone()
+    step((K_steps - 1) % L)
+    torch.cuda.synchronize()
+    graph_ok = bool(torch.equal(graph_out, y_d))
+
+    step_bytes = 2 * linear_bytes(M, Ngu, Kgu) + linear_bytes(M, Nd, Kd)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- dominant kernel: the gate/up GEMV launch, back to back over all layers
+    xq_gu, sa_gu = rt4_amd.quant_act_a8(x_gu)
+    xq_d, sa_d = rt4_amd.quant_act_a8(x_d)
+    gu_mats = [lw[k] for lw in layers for k in ("gate", "up")]
+
+    def gemv_gu():
+        for wq, ws in gu_mats:
+            rt4_amd.gemv_w4a8_q(wq, ws, xq_gu, sa_gu, out=y_g)
+
+    gu_us = timed_graph(torch, gemv_gu) * 1e3 / len(gu_mats)
+    gu_bytes = linear_bytes(M, Ngu, Kgu)
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    roofline = {"kernel": "rt4::gemv_w4a8_k<4,2,false> (gate/up, M=4 K=5120 N=17408)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "us_per_launch": round(gu_us, 3), "bytes_per_launch": gu_bytes,
+                "weight_only_GBs": round((Ngu * Kgu // 2) / (gu_us * 1e-6) / 1e9, 1)}
+
+    kernels = {}
+    if not args.no_extra:
+        d_mats = [lw["down"] for lw in layers]
+
+        def gemv_d():
+            for wq, ws in d_mats:
+                rt4_amd.gemv_w4a8_q(wq, ws, xq_d, sa_d, out=y_d)
+
+        d_us = timed_graph(torch, gemv_d) * 1e3 / len(d_mats)
+        kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(linear_bytes(M, Nd, Kd) / d_us / 1e3, 1)}
+
+        def quant_gu():
+            for _ in range(16):
+                rt4_amd.quant_act_a8(x_gu)
+
+        q_us = timed_graph(torch, quant_gu) * 1e3 / 16
+        kernels["quant_act_m4_k5120"] = {"us": round(q_us, 3)}
+        # M=1 decode (C0 shape 5120x5120) over 16 rotated slices of the gate weights
+        x1 = x_gu[:1].contiguous()
+        xq1, sa1 = rt4_amd.quant_act_a8(x1)
+        c0_mats = [(wq[:5120], ws[:5120]) for wq, ws in gu_mats]
+        y1 = torch.empty((1, 5120), device="cuda")
+
+        def gemv_c0():
+            for wq, ws in c0_mats:
+                rt4_amd.gemv_w4a8_q(wq, ws, xq1, sa1, out=y1)
+
+        c0_us = timed_graph(torch, gemv_c0) * 1e3 / len(c0_mats)
+        kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(linear_bytes(1, 5120, 5120) / c0_us / 1e3, 1)}
+        # LM head (C3): M=4, K=5120, N=248320, two 0.66 GB copies alternated
+        del layers, gu_mats, d_mats, c0_mats
+        torch.cuda.empty_cache()
+        lm = [workload.weights_torch(248320, 5120, generator=gen) for _ in range(2)]
+        y_lm = torch.empty((M, 248320), device="cuda")
+
+        def gemv_lm():
+            for wq, ws in lm:
+                rt4_amd.gemv_w4a8_q(wq, ws, xq_gu, sa_gu, out=y_lm)
+
+        lm_us = timed_graph(torch, gemv_lm) * 1e3 / len(lm)
+        kernels["gemv_lm_head_m4"] = {"us": round(lm_us, 3),
+                                      "GBs": round(linear_bytes(M, 248320, 5120) / lm_us / 1e3, 1)}
+        del lm
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(step_bytes, args.cpu_seconds)
+
+    out = {
+        "metric": metric, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K_steps,
+        "warmup": W_steps, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4*int8->int32", "data": "synthetic",
+        "config": {"workload": "decode MLP step, MTP3 verify width (BASELINE configs[1])", "M": M,
+                   "gate_up_NK": [Ngu, Kgu], "down_NK": [Nd, Kd], "linears_per_step": 3,
+                   "layers_rotated": L, "step_bytes": step_bytes, "graph_matches_eager": graph_ok,
+                   "device": torch.cuda.get_device_name(0)},
+        "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,41 @@
+// rt4_kernels.h -- the reference runtime's kernel API for the RT4 matmul path,
+// implemented by librt4k.so on top of the C ABI in rt4k.h.
+//
+// These are the exact C++ prototypes (names, argument order and meaning,
+// default arguments) of the reference's src/kernels.h, so the reference's
+// src/model.cpp links against librt4k.so without edits.  Behaviour matches the
+// reference wrappers: asynchronous on the null stream, no return value, and a
+// violated precondition or launch failure prints a message and calls exit(1)
+// (src/k_gemv.hip:54-55, :105; src/k_gemm.hip:24-28, :32).
+//
+// The reference's model.cpp includes its own src/kernels.h, which declares the
+// same functions; this header is for other callers.  Do not include both.
+#pragma once
+#include <cstdint>
+
+typedef uint32_t u32;
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+// src/kernels.h:27 -- W4A8 decode GEMV, rows <= 4: y[rows][N] = W[N][K] . x[rows][K].
+// wsc points at the RT4 fp16 row-major scales (typed float* by the reference).
+void k_gemv_w4a8(float* y, const u32* wq, const float* wsc, const float* x, int rows, int N, int K);
+
+// src/kernels.h:32 -- W4A8 prefill GEMM on activations quantized by k_quant_rows_a8.
+// c2 is scratch of at least M*N floats (contents unspecified on return).
+void k_gemm_i4_a8(float* c, float* c2, const u32* wq, const float* wsc_gm, const u32* ah,
+                  const u32* al, const float* sc, const float* sc16, int M, int N, int K);
+
+// src/kernels.h:43 -- 8-bit activation quantizer split into two int4 digits.
+void k_quant_rows_a8(u32* qh, u32* ql, float* sc, float* sc16, const float* x, int rows, int K,
+                     int G, int in_stride = 0, int in_off = 0);
+
+// src/kernels.h:36 -- int4 activation quantizer (RT_ACT4 A/B path).
+void k_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int in_stride = 0,
+                  int in_off = 0);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif

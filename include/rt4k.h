@@ -1,0 +1,123 @@
+/*
+ * rt4k.h -- C ABI of the MI355X (gfx950) RT4 quantized-matmul library, librt4k.so.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is a device pointer
+ * owned by the caller unless stated otherwise; `stream` is a hipStream_t passed
+ * as void* (NULL = the null stream, which is what the reference runtime uses).
+ * Every entry point is asynchronous on `stream` and returns RT4_OK or an error
+ * code; rt4_last_error() then describes the failure (thread-local).
+ *
+ * Formats (docs/FORMAT.md:61-73 of the reference, unchanged here):
+ *   wq   uint32 [N][K/8]   RT4 int4 weights: dword d holds k = 8d..8d+7, nibble e
+ *                          = bits 4e..4e+3, two's complement, low nibble first.
+ *   ws   uint16 [N][K/128] fp16 bit patterns of the per-128-group weight scales,
+ *                          row-major (the reference passes these as `const float*`).
+ *   wsc_gm float [K/128][N] fp32 group-major weight scales (src/model.cpp:190-202).
+ *   xq   int8  [rows][K]   activation codes in "interleaved" order: for each
+ *                          8-element block b, bytes [a(8b+0) a(8b+2) a(8b+4) a(8b+6)
+ *                          a(8b+1) a(8b+3) a(8b+5) a(8b+7)].  Internal to this
+ *                          library; it matches the even/odd nibble split of wq.
+ *
+ * Each entry cites the reference interface it replaces (reference file:line).
+ */
+#ifndef RT4K_H
+#define RT4K_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+#define RT4_OK 0
+#define RT4_E_SHAPE 1    /* a shape precondition of the reference is violated */
+#define RT4_E_ARG 2      /* null pointer, unsupported group size or config */
+#define RT4_E_HIP 3      /* HIP runtime or kernel launch failure */
+
+/* Description of the last failure on this thread ("" if none). */
+const char* rt4_last_error(void);
+/* ABI version of this header (bumped on incompatible change). */
+int rt4_abi_version(void);
+
+/* ------------------------------------------------------------ decode path -- */
+
+/* Decode-side activation quantizer.  Replaces the quant_act launch of
+ * k_gemv_w4a8 (kernels/gemv_w4a8_core.h:34-66, launched at src/k_gemv.hip:70).
+ * x f32 [rows][K] -> xq int8 [rows][K] interleaved, sa f32 [rows][K/128]
+ * (s = amax/127 per group, 1 for an all-zero group), asu int32 [rows][K/128]
+ * = per-group sum of the codes (optional, may be NULL).  K % 128 == 0. */
+int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K,
+                     void* stream);
+
+/* W4A8 GEMV on pre-quantized activations.  Replaces the gemv_w4a8<M,SMEM,NROW>
+ * launch of k_gemv_w4a8 (kernels/gemv_w4a8_core.h:76-209, src/k_gemv.hip:96-103).
+ * y f32 [rows][N] = Σ_g f16(ws[n][g]) * sa[m][g] * Σ_{k∈g} code[n][k]*xq[m][k].
+ * rows in [1,4], K % 128 == 0 (src/k_gemv.hip:54-55). */
+int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                    const float* sa, int rows, int N, int K, void* stream);
+
+/* Same, with an explicit launch configuration (tuning and tests):
+ * tiles = 16-row weight tiles per workgroup (1 or 2), waves = waves per
+ * workgroup splitting K (1..16 for tiles=1, 1..8 for tiles=2). */
+int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                        const float* sa, int rows, int N, int K, int tiles, int waves,
+                        void* stream);
+
+/* Test hook: the same kernel, also writing the exact per-group int32 dot
+ * products gsum int32 [rows][N][K/128] = Σ_{k∈g} code[n][k]*xq[m][k]. */
+int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws,
+                            const int8_t* xq, const float* sa, int rows, int N, int K,
+                            void* stream);
+
+/* The whole decode linear: quantize x, then the GEMV.  Replaces k_gemv_w4a8
+ * (src/kernels.h:27, src/k_gemv.hip:53-106).  x f32 [rows][K] contiguous.
+ * Uses library-owned scratch for the quantized activations, grown with
+ * hipMalloc on first use per device (as the reference does, src/k_gemv.hip:
+ * 56-67); not re-entrant across threads. */
+int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows,
+                  int N, int K, void* stream);
+
+/* ----------------------------------------------------------- prefill path -- */
+
+/* Prefill-side 8-bit quantizer split into two int4 digits.  Replaces
+ * k_quant_rows_a8 (src/kernels.h:43, src/k_new.hip:268-301), same outputs bit
+ * for bit: qh, ql uint32 [rows][K/8] nibble-packed like wq with q8 = 16h + l,
+ * sc, sc16 f32 group-major [K/G][rows], s = amax/119, sc16 = 16*s.
+ * Row r is read at x + r*in_stride + in_off (in_stride 0 means K).
+ * G must be a power of two in [8, 512] dividing K (the runtime uses 128). */
+int rt4_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, const float* x,
+                      int rows, int K, int G, int in_stride, int in_off, void* stream);
+
+/* Same quantizer writing the int8 codes q8 themselves (interleaved [rows][K])
+ * and sc [K/128][rows]: the input of rt4_gemm_w4a8_i8.  No reference
+ * counterpart; it fuses k_quant_rows_a8 with the digit recombination that
+ * rt4_gemm_w4a8 otherwise performs.  G = 128. */
+int rt4_quant_rows_i8(int8_t* xq, float* sc, const float* x, int rows, int K, int in_stride,
+                      int in_off, void* stream);
+
+/* h/l digit planes -> interleaved int8 codes q8 = 16h + l. */
+int rt4_digits_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
+                     void* stream);
+
+/* RT4 fp16 row-major scales -> fp32 group-major.  Replaces the host helper
+ * make_group_major (src/model.cpp:190-202), on the device. */
+int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream);
+
+/* ------------------------------------------- W4A4 siblings (link only) ---- */
+
+/* int4 activation quantizer.  Replaces k_quant_rows (src/kernels.h:36,
+ * src/k_new.hip:192-219): q uint32 [rows][K/8], sc f32 [K/G][rows], s = amax/7. */
+int rt4_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
+                      int in_stride, int in_off, void* stream);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RT4K_H */

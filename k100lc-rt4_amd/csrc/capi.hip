@@ -1,0 +1,206 @@
+// capi.hip -- extern "C" entry points of librt4k.so (declared in include/rt4k.h).
+// Validates shapes the way the reference wrappers do, owns the lazily grown
+// scratch of the composite entry points, and maps failures to status codes.
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+
+#include "rt4_internal.h"
+#include "rt4k.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return RT4_OK;
+    return fail(RT4_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Library-owned device scratch, one buffer per (device, slot), grown on demand.
+// hipFree synchronizes the device, so a buffer still read by queued kernels is
+// never released early.  Not safe for concurrent calls from several threads
+// (the reference's scratch has the same property, src/k_gemv.hip:47-51).
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlots = 3 };
+constexpr int kMaxDev = 64;
+struct Buf {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+std::mutex g_mu;
+Buf g_buf[kMaxDev][kSlots];
+
+int scratch(Slot slot, size_t bytes, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDev) return fail(RT4_E_ARG, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_mu);
+    Buf& b = g_buf[dev][slot];
+    if (b.cap < bytes) {
+        if (b.p) {
+            e = hipFree(b.p);
+            b.p = nullptr;
+            b.cap = 0;
+            if (e != hipSuccess) return hip_status(e, "hipFree(scratch)");
+        }
+        const size_t want = (bytes + 255) & ~size_t(255);
+        e = hipMalloc(&b.p, want);
+        if (e != hipSuccess) return hip_status(e, "hipMalloc(scratch)");
+        b.cap = want;
+    }
+    *out = b.p;
+    return RT4_OK;
+}
+
+int check_gemv_shape(const char* who, int rows, int N, int K) {
+    if (rows < 1 || rows > 4) return fail(RT4_E_SHAPE, "%s: rows=%d not in [1,4] (prefill uses the GEMM)", who, rows);
+    if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "%s: K=%d is not a positive multiple of 128", who, K);
+    if (N <= 0) return fail(RT4_E_SHAPE, "%s: N=%d must be positive", who, N);
+    // the quantized activations of a call are staged whole in one workgroup's LDS
+    if ((size_t)rows * K > rt4::kGemvMaxActBytes)
+        return fail(RT4_E_SHAPE, "%s: rows*K=%lld exceeds the %d-byte activation stage", who,
+                    (long long)rows * K, (int)rt4::kGemvMaxActBytes);
+    return RT4_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// The GEMV reads weights and activations with 16-byte vector loads.
+int check_gemv_align(const char* who, const void* y, const uint32_t* wq, const uint16_t* ws,
+                     const int8_t* xq, const float* sa) {
+    if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
+        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
+    return RT4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rt4_last_error(void) { return g_err; }
+int rt4_abi_version(void) { return 1; }
+
+int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K,
+                     void* stream) {
+    if (!xq || !sa || !x) return fail(RT4_E_ARG, "rt4_quant_act_a8: null pointer");
+    if (rows < 1 || rows > 65535) return fail(RT4_E_SHAPE, "rt4_quant_act_a8: rows=%d", rows);
+    if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "rt4_quant_act_a8: K=%d is not a positive multiple of 128", K);
+    if (!aligned(xq, 8) || !aligned(x, 4) || !aligned(sa, 4) || !aligned(asu, 4))
+        return fail(RT4_E_ARG, "rt4_quant_act_a8: misaligned pointer (xq needs 8 bytes)");
+    return hip_status(rt4::launch_quant_act_a8(xq, sa, asu, x, rows, K, as_stream(stream)),
+                      "rt4_quant_act_a8 launch");
+}
+
+int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                        const float* sa, int rows, int N, int K, int tiles, int waves,
+                        void* stream) {
+    if (!y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_w4a8", rows, N, K);
+    if (rc || (rc = check_gemv_align("rt4_gemv_w4a8", y, wq, ws, xq, sa))) return rc;
+    rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    if (tiles > 0) c.rt = tiles;
+    if (waves > 0) c.waves = waves;
+    if (!rt4::gemv_cfg_valid(c, K)) return fail(RT4_E_ARG, "rt4_gemv_w4a8: bad config tiles=%d waves=%d", c.rt, c.waves);
+    return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, xq, sa, rows, N, K, c, as_stream(stream)),
+                      "rt4_gemv_w4a8 launch");
+}
+
+int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                    const float* sa, int rows, int N, int K, void* stream) {
+    return rt4_gemv_w4a8_q_cfg(y, wq, ws, xq, sa, rows, N, K, 0, 0, stream);
+}
+
+int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws,
+                            const int8_t* xq, const float* sa, int rows, int N, int K,
+                            void* stream) {
+    if (!gsum || !y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8_groupsums: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_w4a8_groupsums", rows, N, K);
+    if (rc || (rc = check_gemv_align("rt4_gemv_w4a8_groupsums", y, wq, ws, xq, sa))) return rc;
+    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    return hip_status(rt4::launch_gemv_w4a8(y, gsum, wq, ws, xq, sa, rows, N, K, c, as_stream(stream)),
+                      "rt4_gemv_w4a8_groupsums launch");
+}
+
+int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows,
+                  int N, int K, void* stream) {
+    if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
+    int rc = check_gemv_shape("k_gemv_w4a8", rows, N, K);
+    if (rc) return rc;
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
+        return fail(RT4_E_ARG, "k_gemv_w4a8: misaligned pointer (wq needs 16 bytes)");
+    void *q = nullptr, *s = nullptr;
+    if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q))) return rc;
+    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s))) return rc;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = rt4::launch_quant_act_a8(static_cast<int8_t*>(q), static_cast<float*>(s), nullptr, x, rows, K, st);
+    if (e != hipSuccess) return hip_status(e, "k_gemv_w4a8 quant launch");
+    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, static_cast<const int8_t*>(q),
+                                            static_cast<const float*>(s), rows, N, K, c, st),
+                      "k_gemv_w4a8 launch");
+}
+
+int rt4_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, const float* x,
+                      int rows, int K, int G, int in_stride, int in_off, void* stream) {
+    if (!qh || !ql || !sc || !sc16 || !x) return fail(RT4_E_ARG, "rt4_quant_rows_a8: null pointer");
+    if (!rt4::quant_group_supported(G) || K <= 0 || K % G)
+        return fail(RT4_E_ARG, "rt4_quant_rows_a8: group G=%d unsupported for K=%d", G, K);
+    if (rows < 1 || rows > 65535 || in_stride < 0 || in_off < 0)
+        return fail(RT4_E_SHAPE, "rt4_quant_rows_a8: rows=%d in_stride=%d in_off=%d", rows, in_stride, in_off);
+    return hip_status(rt4::launch_quant_rows_a8(qh, ql, sc, sc16, nullptr, x, rows, K, G, in_stride, in_off,
+                                                as_stream(stream)),
+                      "rt4_quant_rows_a8 launch");
+}
+
+int rt4_quant_rows_i8(int8_t* xq, float* sc, const float* x, int rows, int K, int in_stride,
+                      int in_off, void* stream) {
+    if (!xq || !sc || !x) return fail(RT4_E_ARG, "rt4_quant_rows_i8: null pointer");
+    if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "rt4_quant_rows_i8: K=%d is not a positive multiple of 128", K);
+    if (rows < 1 || rows > 65535 || in_stride < 0 || in_off < 0)
+        return fail(RT4_E_SHAPE, "rt4_quant_rows_i8: rows=%d in_stride=%d in_off=%d", rows, in_stride, in_off);
+    if (!aligned(xq, 8) || !aligned(x, 4) || !aligned(sc, 4))
+        return fail(RT4_E_ARG, "rt4_quant_rows_i8: misaligned pointer (xq needs 8 bytes)");
+    return hip_status(rt4::launch_quant_rows_a8(nullptr, nullptr, sc, nullptr, xq, x, rows, K, 128, in_stride,
+                                                in_off, as_stream(stream)),
+                      "rt4_quant_rows_i8 launch");
+}
+
+int rt4_digits_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
+                     void* stream) {
+    if (!xq || !qh || !ql) return fail(RT4_E_ARG, "rt4_digits_to_i8: null pointer");
+    if (rows < 1 || K <= 0 || K % 8) return fail(RT4_E_SHAPE, "rt4_digits_to_i8: rows=%d K=%d", rows, K);
+    if (!aligned(xq, 8) || !aligned(qh, 4) || !aligned(ql, 4))
+        return fail(RT4_E_ARG, "rt4_digits_to_i8: misaligned pointer (xq needs 8 bytes)");
+    return hip_status(rt4::launch_hl_to_i8(xq, qh, ql, rows, K, as_stream(stream)), "rt4_digits_to_i8 launch");
+}
+
+int rt4_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
+                      int in_stride, int in_off, void* stream) {
+    if (!q || !sc || !x) return fail(RT4_E_ARG, "rt4_quant_rows_a4: null pointer");
+    if (!rt4::quant_group_supported(G) || K <= 0 || K % G)
+        return fail(RT4_E_ARG, "rt4_quant_rows_a4: group G=%d unsupported for K=%d", G, K);
+    if (rows < 1 || rows > 65535 || in_stride < 0 || in_off < 0)
+        return fail(RT4_E_SHAPE, "rt4_quant_rows_a4: rows=%d in_stride=%d in_off=%d", rows, in_stride, in_off);
+    return hip_status(rt4::launch_quant_rows_a4(q, sc, x, rows, K, G, in_stride, in_off, as_stream(stream)),
+                      "rt4_quant_rows_a4 launch");
+}
+
+int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream) {
+    if (!wsc_gm || !ws) return fail(RT4_E_ARG, "rt4_make_group_major: null pointer");
+    if (N <= 0 || K <= 0 || K % 128) return fail(RT4_E_SHAPE, "rt4_make_group_major: N=%d K=%d", N, K);
+    return hip_status(rt4::launch_make_group_major(wsc_gm, ws, N, K / 128, as_stream(stream)),
+                      "rt4_make_group_major launch");
+}
+
+}  // extern "C"

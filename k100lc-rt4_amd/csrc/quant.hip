@@ -1,0 +1,237 @@
+// quant.hip -- activation quantizers of the RT4 path, gfx950.
+//
+// Three reference quantizers are restated here; each must produce bit-identical
+// integer codes and scales, so every step uses the same IEEE single operations
+// as the reference (correctly rounded division -- hipcc's default -- and
+// round-half-to-even lrintf).  One lane owns 8 consecutive elements of a row,
+// so a G-element group is an aligned run of G/8 lanes and its max-abs is a
+// short xor-shuffle reduction; loads and stores are full dwords.
+#include "rt4_dev.h"
+#include "rt4_internal.h"
+
+namespace rt4 {
+
+// Load 8 consecutive floats; vector loads when the address is 16-byte aligned.
+__device__ __forceinline__ void load8(const float* p, bool aligned, float v[8]) {
+    if (aligned) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0];
+        const float4 b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = p[e];
+    }
+}
+
+// Eight int8 codes -> two dwords in the interleaved order [c0 c2 c4 c6 | c1 c3 c5 c7].
+__device__ __forceinline__ uint2 interleave8(const int c[8]) {
+    uint2 r;
+    r.x = (uint32_t)(c[0] & 0xFF) | (uint32_t)(c[2] & 0xFF) << 8 | (uint32_t)(c[4] & 0xFF) << 16 |
+          (uint32_t)(c[6] & 0xFF) << 24;
+    r.y = (uint32_t)(c[1] & 0xFF) | (uint32_t)(c[3] & 0xFF) << 8 | (uint32_t)(c[5] & 0xFF) << 16 |
+          (uint32_t)(c[7] & 0xFF) << 24;
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Decode-side quantizer (restates quant_act, kernels/gemv_w4a8_core.h:34-66):
+// per (row, 128-group) s = amax>0 ? amax/127 : 1, q = clamp(lrintf(x/s), -128, 127).
+// Outputs: xq int8 [rows][K] interleaved, sa f32 [rows][K/128], and optionally
+// asu = Σq per group (the reference needs it for its u=code+8 correction; the
+// MFMA GEMV here does not, but it is kept for parity checks).
+// grid (ceil(K/8/256), rows), block 256.
+__global__ __launch_bounds__(256) void quant_act_a8_k(const float* __restrict__ x,
+                                                      int8_t* __restrict__ xq,
+                                                      float* __restrict__ sa,
+                                                      int32_t* __restrict__ asu, int K,
+                                                      int x_aligned) {
+    const int m = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;  // 8-element block in the row
+    if (i >= (K >> 3)) return;                     // K%128==0: whole 16-lane runs exit together
+    float v[8];
+    load8(x + (size_t)m * K + 8 * (size_t)i, x_aligned, v);
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = run_max<16>(amax);
+    const float s = amax > 0.f ? amax / 127.f : 1.f;
+    int c[8];
+    int part = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        c[e] = clampi((int)lrintf(v[e] / s), -128, 127);
+        part += c[e];
+    }
+    *reinterpret_cast<uint2*>(xq + (size_t)m * K + 8 * (size_t)i) = interleave8(c);
+    const int NG = K >> 7;
+    if ((i & 15) == 0) sa[(size_t)m * NG + (i >> 4)] = s;
+    if (asu) {
+        part = run_sum<16>(part);
+        if ((i & 15) == 0) asu[(size_t)m * NG + (i >> 4)] = part;
+    }
+}
+
+hipError_t launch_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows,
+                               int K, hipStream_t st) {
+    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int aligned = ((uintptr_t)x & 15) == 0;
+    hipLaunchKernelGGL(quant_act_a8_k, grid, dim3(256), 0, st, x, xq, sa, asu, K, aligned);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Prefill-side quantizer (restates quant_rows_a8_k, src/k_new.hip:268-301):
+// per (row, G-group) s = amax>0 ? amax/119 : 1, q8 = clamp(lrintf(x/s), -128, 119),
+// h = (q8+8)>>4, l = q8-16h.  Outputs the reference's layout: qh, ql u32
+// [rows][K/8] nibble-packed like RT4 weights, sc and sc16 = 16*sc f32 group-major
+// [K/G][rows].  Optionally also writes the int8 code q8 itself, interleaved
+// [rows][K], which is what the MFMA GEMM consumes.
+// GL = G/8 lanes per group.  grid (ceil(K/8/256), rows), block 256.
+template <int GL>
+__global__ __launch_bounds__(256) void quant_rows_a8_k(
+    const float* __restrict__ x, uint32_t* __restrict__ qh, uint32_t* __restrict__ ql,
+    float* __restrict__ sc, float* __restrict__ sc16, int8_t* __restrict__ xq, int rows, int K,
+    int in_stride, int in_off, int x_aligned) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= (K >> 3)) return;  // K%G==0: whole GL-lane runs exit together
+    float v[8];
+    load8(x + (size_t)r * in_stride + in_off + 8 * (size_t)i, x_aligned, v);
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = run_max<GL>(amax);
+    const float s = amax > 0.f ? amax / 119.f : 1.f;
+    uint32_t wh = 0, wl = 0;
+    int c[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int q8 = clampi((int)lrintf(v[e] / s), -128, 119);
+        const int h = (q8 + 8) >> 4;  // floor, also for negatives
+        const int l = q8 - 16 * h;    // in [-8, 7]
+        wh |= (uint32_t)(h & 0xF) << (4 * e);
+        wl |= (uint32_t)(l & 0xF) << (4 * e);
+        c[e] = q8;
+    }
+    const size_t d = (size_t)r * (K >> 3) + i;
+    if (qh) qh[d] = wh;
+    if (ql) ql[d] = wl;
+    if (i % GL == 0) {
+        const size_t gi = (size_t)(i / GL) * rows + r;
+        if (sc) sc[gi] = s;
+        if (sc16) sc16[gi] = s * 16.f;
+    }
+    if (xq) *reinterpret_cast<uint2*>(xq + (size_t)r * K + 8 * (size_t)i) = interleave8(c);
+}
+
+// int4 activation quantizer (restates quant_rows_k, src/k_new.hip:192-219):
+// s = amax>0 ? amax/7 : 1, c = clamp(lrintf(x/s), -8, 7), nibble-packed, sc group-major.
+template <int GL>
+__global__ __launch_bounds__(256) void quant_rows_a4_k(const float* __restrict__ x,
+                                                       uint32_t* __restrict__ q,
+                                                       float* __restrict__ sc, int rows, int K,
+                                                       int in_stride, int in_off, int x_aligned) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= (K >> 3)) return;
+    float v[8];
+    load8(x + (size_t)r * in_stride + in_off + 8 * (size_t)i, x_aligned, v);
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = run_max<GL>(amax);
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int cc = clampi((int)lrintf(v[e] / s), -8, 7);
+        w |= (uint32_t)(cc & 0xF) << (4 * e);
+    }
+    q[(size_t)r * (K >> 3) + i] = w;
+    if (i % GL == 0) sc[(size_t)(i / GL) * rows + r] = s;
+}
+
+#define RT4_GL_CASES(KERNEL, ...)                                                         \
+    switch (G / 8) {                                                                      \
+        case 1: hipLaunchKernelGGL(KERNEL<1>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 2: hipLaunchKernelGGL(KERNEL<2>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 4: hipLaunchKernelGGL(KERNEL<4>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 8: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 16: hipLaunchKernelGGL(KERNEL<16>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 32: hipLaunchKernelGGL(KERNEL<32>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 64: hipLaunchKernelGGL(KERNEL<64>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        default: return hipErrorInvalidValue;                                             \
+    }
+
+bool quant_group_supported(int G) {
+    return G >= 8 && G <= 512 && (G & (G - 1)) == 0;
+}
+
+hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, int8_t* xq,
+                                const float* x, int rows, int K, int G, int in_stride, int in_off,
+                                hipStream_t st) {
+    if (in_stride == 0) in_stride = K;
+    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int aligned = (((uintptr_t)(x + in_off)) & 15) == 0 && (in_stride % 4) == 0;
+    RT4_GL_CASES(quant_rows_a8_k, x, qh, ql, sc, sc16, xq, rows, K, in_stride, in_off, aligned);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
+                                int in_stride, int in_off, hipStream_t st) {
+    if (in_stride == 0) in_stride = K;
+    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int aligned = (((uintptr_t)(x + in_off)) & 15) == 0 && (in_stride % 4) == 0;
+    RT4_GL_CASES(quant_rows_a4_k, x, q, sc, rows, K, in_stride, in_off, aligned);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// h/l digit planes -> int8 codes q8 = 16h + l, interleaved, for the MFMA GEMM.
+// Bytewise: x = (h<<4) | (l^8) is q8+8 with no carries between bytes; the
+// per-byte subtraction of 8 then uses the borrow-free SWAR form
+// ((x | 0x80..) - 0x08..) ^ (~x & 0x80..).  One lane per dword pair.
+__device__ __forceinline__ uint32_t swar_sub8(uint32_t x) {
+    return ((x | 0x80808080u) - 0x08080808u) ^ (~x & 0x80808080u);
+}
+
+__global__ __launch_bounds__(256) void hl_to_i8_k(const uint32_t* __restrict__ qh,
+                                                  const uint32_t* __restrict__ ql,
+                                                  int8_t* __restrict__ xq, size_t ndw) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= ndw) return;
+    const uint32_t h = qh[i], l = ql[i] ^ 0x88888888u;
+    const uint32_t xe = ((h << 4) & 0xF0F0F0F0u) | (l & 0x0F0F0F0Fu);
+    const uint32_t xo = (h & 0xF0F0F0F0u) | ((l >> 4) & 0x0F0F0F0Fu);
+    reinterpret_cast<uint2*>(xq)[i] = make_uint2(swar_sub8(xe), swar_sub8(xo));
+}
+
+hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
+                           hipStream_t st) {
+    const size_t ndw = (size_t)rows * (K / 8);
+    const unsigned blocks = (unsigned)((ndw + 255) / 256);
+    hipLaunchKernelGGL(hl_to_i8_k, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// RT4 fp16 row-major weight scales -> fp32 group-major (src/model.cpp:190-202,
+// a host loop in the reference).  One thread per output element; writes are
+// coalesced, reads stride by NG.
+__global__ __launch_bounds__(256) void make_group_major_k(const uint16_t* __restrict__ ws,
+                                                          float* __restrict__ out, int N, int NG) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)N * NG) return;
+    const int g = (int)(i / N), n = (int)(i % N);
+    out[i] = f16_bits_to_f32(ws[(size_t)n * NG + g]);
+}
+
+hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG, hipStream_t st) {
+    const size_t tot = (size_t)N * NG;
+    hipLaunchKernelGGL(make_group_major_k, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, ws, out,
+                       N, NG);
+    return hipGetLastError();
+}
+
+}  // namespace rt4

@@ -1,0 +1,52 @@
+// rt4_dev.h -- device-side building blocks shared by the RT4 kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace rt4 {
+
+constexpr int kGroup = 128;       // RT4 quantization group along K (docs/FORMAT.md:61-73)
+constexpr int kWave = 64;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// fp16 bit pattern -> fp32 (exact).
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+// Wave-uniform value as an SGPR (lets loads indexed by it become scalar loads).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Max / sum across an aligned run of `W` lanes (W a power of two, <= 64).
+template <int W>
+__device__ __forceinline__ float run_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+template <int W>
+__device__ __forceinline__ int run_sum(int v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// int4 -> int8 unpack used by every MFMA kernel here.  An RT4 dword holds
+// codes k=8d..8d+7 as nibbles, low nibble first, two's complement.  Shifting a
+// nibble into the high half of a byte gives that byte the signed value 16*code
+// exactly, so:
+//   even(w): bytes = 16*code[8d+0,2,4,6]      odd(w): bytes = 16*code[8d+1,3,5,7]
+// Every MFMA over these operands therefore returns 16x the integer dot product,
+// which an arithmetic shift (or a 1/16 folded into an fp32 scale) removes
+// exactly.  Activations are stored in the matching "interleaved" byte order:
+// for each 8-element block, [a0 a2 a4 a6 | a1 a3 a5 a7].
+__device__ __forceinline__ uint32_t even_x16(uint32_t w) { return (w << 4) & 0xF0F0F0F0u; }
+__device__ __forceinline__ uint32_t odd_x16(uint32_t w) { return w & 0xF0F0F0F0u; }
+
+// Saturating helpers for the quantizers (same clamp order as the reference).
+__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v > hi ? hi : (v < lo ? lo : v); }
+
+}  // namespace rt4

@@ -1,0 +1,208 @@
+"""rt4_amd -- Python host side of the MI355X RT4 quantized-matmul library.
+
+The compute lives in ``lib/librt4k.so`` (hand-written HIP for gfx950, C ABI in
+``include/rt4k.h``).  This module binds that ABI with ctypes and offers thin
+wrappers over torch device tensors (torch is used for device memory and streams
+only).  There is no fallback: if the library is missing, every call raises.
+
+Reference interface mirrored (src/kernels.h of K100LC-RT4):
+    k_gemv_w4a8      -> gemv_w4a8            (src/kernels.h:27)
+    k_quant_rows_a8  -> quant_rows_a8        (src/kernels.h:43)
+    k_gemm_i4_a8     -> gemm_w4a8            (src/kernels.h:32)
+    k_quant_rows     -> quant_rows_a4        (src/kernels.h:36)
+plus the pieces those wrappers launch internally (quant_act_a8, gemv_w4a8_q).
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+from . import layout  # noqa: F401  (re-exported helpers)
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "librt4k.so"
+GROUP = 128
+
+# Every symbol include/rt4k.h declares (checked by the CPU test suite).
+C_EXPORTS = (
+    "rt4_last_error", "rt4_abi_version",
+    "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_w4a8_groupsums",
+    "rt4_gemv_w4a8", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
+    "rt4_make_group_major", "rt4_quant_rows_a4",
+)
+# The reference-compatible C++ entry points (include/rt4_kernels.h), mangled.
+CXX_EXPORTS = (
+    "_Z11k_gemv_w4a8PfPKjPKfS3_iii",
+    "_Z15k_quant_rows_a8PjS_PfS0_PKfiiiii",
+    "_Z12k_quant_rowsPjPfPKfiiiii",
+)
+
+
+class RT4Error(RuntimeError):
+    """A librt4k entry point returned an error status."""
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGS = {
+    "rt4_quant_act_a8": [_P, _P, _P, _P, _I, _I, _P],
+    "rt4_gemv_w4a8_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a8": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_quant_rows_a8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "rt4_quant_rows_i8": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "rt4_digits_to_i8": [_P, _P, _P, _I, _I, _P],
+    "rt4_make_group_major": [_P, _P, _I, _I, _P],
+    "rt4_quant_rows_a4": [_P, _P, _P, _I, _I, _I, _I, _I, _P],
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load librt4k.so once (no GPU work happens at load time)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RT4Error(f"{LIB_PATH} is missing: build it with `make -C k100lc-rt4_amd` "
+                           "or __graft_entry__.build()")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.rt4_last_error.restype = ctypes.c_char_p
+        L.rt4_last_error.argtypes = []
+        L.rt4_abi_version.restype = ctypes.c_int
+        for name, args in _SIGS.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise RT4Error(lib().rt4_last_error().decode(errors="replace"))
+
+
+# ----------------------------------------------------------- torch helpers --
+def _torch():
+    import torch
+    return torch
+
+
+def _stream():
+    return _P(_torch().cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RT4Error("rt4_amd expects device tensors")
+    if not t.is_contiguous():
+        raise RT4Error("rt4_amd expects contiguous tensors")
+    return _P(t.data_ptr())
+
+
+def _empty(shape, dtype, device):
+    return _torch().empty(shape, dtype=dtype, device=device)
+
+
+# ---------------------------------------------------------------- decode ----
+def quant_act_a8(x, want_sums: bool = False):
+    """x f32 [rows, K] -> (xq int8 [rows, K] interleaved, sa f32 [rows, K/128][, asu])."""
+    torch = _torch()
+    rows, K = x.shape
+    xq = _empty((rows, K), torch.int8, x.device)
+    sa = _empty((rows, K // GROUP), torch.float32, x.device)
+    asu = _empty((rows, K // GROUP), torch.int32, x.device) if want_sums else None
+    _check(lib().rt4_quant_act_a8(_ptr(xq), _ptr(sa), _ptr(asu), _ptr(x), rows, K, _stream()))
+    return (xq, sa, asu) if want_sums else (xq, sa)
+
+
+def gemv_w4a8_q(wq, ws, xq, sa, out=None, tiles: int = 0, waves: int = 0):
+    """W4A8 GEMV on quantized activations.  wq int32/uint32 [N, K/8], ws int16/fp16 [N, K/128]."""
+    torch = _torch()
+    rows, K = xq.shape
+    N = wq.shape[0]
+    y = out if out is not None else _empty((rows, N), torch.float32, xq.device)
+    _check(lib().rt4_gemv_w4a8_q_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(xq), _ptr(sa), rows, N, K,
+                                     tiles, waves, _stream()))
+    return y
+
+
+def gemv_w4a8_groupsums(wq, ws, xq, sa):
+    """Same kernel, returning (y, gsum int32 [rows, N, K/128])."""
+    torch = _torch()
+    rows, K = xq.shape
+    N = wq.shape[0]
+    y = _empty((rows, N), torch.float32, xq.device)
+    gs = _empty((rows, N, K // GROUP), torch.int32, xq.device)
+    _check(lib().rt4_gemv_w4a8_groupsums(_ptr(gs), _ptr(y), _ptr(wq), _ptr(ws), _ptr(xq), _ptr(sa),
+                                         rows, N, K, _stream()))
+    return y, gs
+
+
+def gemv_w4a8(wq, ws, x, out=None):
+    """Drop-in k_gemv_w4a8: quantize x f32 [rows, K] and multiply (rows <= 4)."""
+    torch = _torch()
+    rows, K = x.shape
+    N = wq.shape[0]
+    y = out if out is not None else _empty((rows, N), torch.float32, x.device)
+    _check(lib().rt4_gemv_w4a8(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, _stream()))
+    return y
+
+
+# --------------------------------------------------------------- prefill ----
+def quant_rows_a8(x, rows: int | None = None, K: int | None = None, G: int = GROUP,
+                  in_stride: int = 0, in_off: int = 0):
+    """Drop-in k_quant_rows_a8 -> (qh, ql int32 [rows, K/8], sc, sc16 f32 [K/G, rows])."""
+    torch = _torch()
+    if rows is None or K is None:
+        rows, K = x.shape
+    qh = _empty((rows, K // 8), torch.int32, x.device)
+    ql = _empty((rows, K // 8), torch.int32, x.device)
+    sc = _empty((K // G, rows), torch.float32, x.device)
+    sc16 = _empty((K // G, rows), torch.float32, x.device)
+    _check(lib().rt4_quant_rows_a8(_ptr(qh), _ptr(ql), _ptr(sc), _ptr(sc16), _ptr(x), rows, K, G,
+                                   in_stride, in_off, _stream()))
+    return qh, ql, sc, sc16
+
+
+def quant_rows_i8(x, rows: int | None = None, K: int | None = None, in_stride: int = 0,
+                  in_off: int = 0):
+    """Same quantizer -> (xq int8 [rows, K] interleaved, sc f32 [K/128, rows])."""
+    torch = _torch()
+    if rows is None or K is None:
+        rows, K = x.shape
+    xq = _empty((rows, K), torch.int8, x.device)
+    sc = _empty((K // GROUP, rows), torch.float32, x.device)
+    _check(lib().rt4_quant_rows_i8(_ptr(xq), _ptr(sc), _ptr(x), rows, K, in_stride, in_off, _stream()))
+    return xq, sc
+
+
+def digits_to_i8(qh, ql):
+    torch = _torch()
+    rows, KD = qh.shape
+    xq = _empty((rows, KD * 8), torch.int8, qh.device)
+    _check(lib().rt4_digits_to_i8(_ptr(xq), _ptr(qh), _ptr(ql), rows, KD * 8, _stream()))
+    return xq
+
+
+def make_group_major(ws, K: int):
+    torch = _torch()
+    N = ws.shape[0]
+    out = _empty((K // GROUP, N), torch.float32, ws.device)
+    _check(lib().rt4_make_group_major(_ptr(out), _ptr(ws), N, K, _stream()))
+    return out
+
+
+def quant_rows_a4(x, rows: int | None = None, K: int | None = None, G: int = GROUP,
+                  in_stride: int = 0, in_off: int = 0):
+    """Drop-in k_quant_rows -> (q int32 [rows, K/8], sc f32 [K/G, rows])."""
+    torch = _torch()
+    if rows is None or K is None:
+        rows, K = x.shape
+    q = _empty((rows, K // 8), torch.int32, x.device)
+    sc = _empty((K // G, rows), torch.float32, x.device)
+    _check(lib().rt4_quant_rows_a4(_ptr(q), _ptr(sc), _ptr(x), rows, K, G, in_stride, in_off,
+                                   _stream()))
+    return q, sc

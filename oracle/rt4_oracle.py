@@ -1,0 +1,182 @@
+"""ctypes front end of liboracle.so -- the C restatement in rt4_oracle.c.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Each wrapper names the
+reference function it restates; the C file cites file:line for every step.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+GROUP = 128
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE), "oracle"], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        P, I = ctypes.c_void_p, ctypes.c_int
+        sig = {
+            "rt4o_f16_to_f32": ([ctypes.c_uint16], ctypes.c_float),
+            "rt4o_dot8_i4": ([ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int32], ctypes.c_int32),
+            "rt4o_quant_act": ([P, I, I, P, P, P], None),
+            "rt4o_quant_rows_a8": ([P, I, I, I, I, I, P, P, P, P], None),
+            "rt4o_quant_rows_i8": ([P, I, I, I, I, I, P, P], None),
+            "rt4o_quant_rows_a4": ([P, I, I, I, I, I, P, P], None),
+            "rt4o_make_group_major": ([P, I, I, P], None),
+            "rt4o_gemv_groupsums": ([P, P, I, I, I, P], None),
+            "rt4o_gemv_fold": ([P, P, P, I, I, I, P], None),
+            "rt4o_gemv_w4a8": ([P, P, P, I, I, I, P], None),
+            "rt4o_gemm_w4a8_points": ([P, P, P, P, P, P, I, I, I, P, P, I, P, P], None),
+            "rt4o_gemm_w4a4_points": ([P, P, P, P, I, I, I, P, P, I, P, P], None),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def f16_to_f32(h: int) -> float:
+    return lib().rt4o_f16_to_f32(h)
+
+
+def dot8_i4(a: int, b: int, acc: int = 0) -> int:
+    """v_dot8_i32_i4 semantics (bench/bench_isa2.cpp:128-145)."""
+    return lib().rt4o_dot8_i4(a & 0xFFFFFFFF, b & 0xFFFFFFFF, acc)
+
+
+def quant_act(x: np.ndarray):
+    """quant_act (kernels/gemv_w4a8_core.h:34-66) -> (q int8 [M,K] natural, sa [M,NG], asu [M,NG])."""
+    x = _c(x, np.float32)
+    M, K = x.shape
+    q = np.empty((M, K), np.int8)
+    sa = np.empty((M, K // GROUP), np.float32)
+    asu = np.empty((M, K // GROUP), np.int32)
+    lib().rt4o_quant_act(_p(x), M, K, _p(q), _p(sa), _p(asu))
+    return q, sa, asu
+
+
+def quant_rows_a8(x: np.ndarray, rows: int, K: int, G: int = GROUP, in_stride: int = 0,
+                  in_off: int = 0):
+    """quant_rows_a8_k (src/k_new.hip:268-301) -> (qh, ql uint32 [rows,K/8], sc, sc16 [K/G,rows])."""
+    x = _c(x, np.float32)
+    qh = np.empty((rows, K // 8), np.uint32)
+    ql = np.empty((rows, K // 8), np.uint32)
+    sc = np.empty((K // G, rows), np.float32)
+    sc16 = np.empty((K // G, rows), np.float32)
+    lib().rt4o_quant_rows_a8(_p(x), rows, K, G, in_stride, in_off, _p(qh), _p(ql), _p(sc), _p(sc16))
+    return qh, ql, sc, sc16
+
+
+def quant_rows_i8(x: np.ndarray, rows: int, K: int, G: int = GROUP, in_stride: int = 0,
+                  in_off: int = 0):
+    """The same quantizer's int8 code q8 = 16h + l (natural order) and sc."""
+    x = _c(x, np.float32)
+    q = np.empty((rows, K), np.int8)
+    sc = np.empty((K // G, rows), np.float32)
+    lib().rt4o_quant_rows_i8(_p(x), rows, K, G, in_stride, in_off, _p(q), _p(sc))
+    return q, sc
+
+
+def quant_rows_a4(x: np.ndarray, rows: int, K: int, G: int = GROUP, in_stride: int = 0,
+                  in_off: int = 0):
+    """quant_rows_k (src/k_new.hip:192-219) -> (q uint32 [rows,K/8], sc [K/G,rows])."""
+    x = _c(x, np.float32)
+    q = np.empty((rows, K // 8), np.uint32)
+    sc = np.empty((K // G, rows), np.float32)
+    lib().rt4o_quant_rows_a4(_p(x), rows, K, G, in_stride, in_off, _p(q), _p(sc))
+    return q, sc
+
+
+def make_group_major(ws: np.ndarray) -> np.ndarray:
+    """make_group_major (src/model.cpp:190-202): uint16 [N,NG] -> f32 [NG,N]."""
+    ws = _c(ws, np.uint16)
+    N, NG = ws.shape
+    out = np.empty((NG, N), np.float32)
+    lib().rt4o_make_group_major(_p(ws), N, NG, _p(out))
+    return out
+
+
+def gemv_groupsums(wq: np.ndarray, q: np.ndarray) -> np.ndarray:
+    """Exact I[m][n][g] = Σ code*q over each 128-group (q in natural order)."""
+    wq = _c(wq, np.uint32)
+    q = _c(q, np.int8)
+    M, K = q.shape
+    N = wq.shape[0]
+    I = np.empty((M, N, K // GROUP), np.int32)
+    lib().rt4o_gemv_groupsums(_p(wq), _p(q), M, N, K, _p(I))
+    return I
+
+
+def gemv_fold(I: np.ndarray, ws: np.ndarray, sa: np.ndarray) -> np.ndarray:
+    """fp64 Σ_g f16(ws)*sa*I (kernels/gemv_w4a8_core.h:189-197)."""
+    I = _c(I, np.int32)
+    ws = _c(ws, np.uint16)
+    sa = _c(sa, np.float32)
+    M, N, NG = I.shape
+    y = np.empty((M, N), np.float64)
+    lib().rt4o_gemv_fold(_p(I), _p(ws), _p(sa), M, N, NG * GROUP, _p(y))
+    return y
+
+
+def gemv_w4a8(wq: np.ndarray, ws: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """k_gemv_w4a8 (src/k_gemv.hip:53-106) end to end, fp64 result."""
+    wq = _c(wq, np.uint32)
+    ws = _c(ws, np.uint16)
+    x = _c(x, np.float32)
+    M, K = x.shape
+    N = wq.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().rt4o_gemv_w4a8(_p(wq), _p(ws), _p(x), M, N, K, _p(y))
+    return y
+
+
+def gemm_w4a8_points(wq, sb, ah, al, sc, sc16, M, N, K, mi, ni):
+    """k_gemm_i4_a8 (src/k_gemm.hip:22-34) at points (mi[p], ni[p]) -> (c fp64 [P], Ig int32 [P,NG])."""
+    mi = _c(mi, np.int32)
+    ni = _c(ni, np.int32)
+    P = mi.size
+    c = np.empty(P, np.float64)
+    Ig = np.empty((P, K // GROUP), np.int32)
+    lib().rt4o_gemm_w4a8_points(_p(_c(wq, np.uint32)), _p(_c(sb, np.float32)), _p(_c(ah, np.uint32)),
+                                _p(_c(al, np.uint32)), _p(_c(sc, np.float32)), _p(_c(sc16, np.float32)),
+                                M, N, K, _p(mi), _p(ni), P, _p(c), _p(Ig))
+    return c, Ig
+
+
+def gemm_w4a4_points(wq, sb, aq, sa, M, N, K, mi, ni):
+    """k_gemm_i4 (src/k_gemm.hip:8-17) at points -> (c fp64 [P], Ig int32 [P,NG])."""
+    mi = _c(mi, np.int32)
+    ni = _c(ni, np.int32)
+    P = mi.size
+    c = np.empty(P, np.float64)
+    Ig = np.empty((P, K // GROUP), np.int32)
+    lib().rt4o_gemm_w4a4_points(_p(_c(wq, np.uint32)), _p(_c(sb, np.float32)), _p(_c(aq, np.uint32)),
+                                _p(_c(sa, np.float32)), M, N, K, _p(mi), _p(ni), P, _p(c), _p(Ig))
+    return c, Ig

@@ -1,0 +1,89 @@
+"""CPU tests of the C ABI boundary: load, exports, precondition errors.
+
+No kernel is launched here: every call below fails its shape or argument check
+before any HIP call, exactly where the reference's wrappers would exit(1).
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "rt4k.h"
+
+
+def declared_c_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:const char\*|int)\s+(rt4_\w+)\(", text, flags=re.M)))
+
+
+def test_header_and_binding_agree(rt4):
+    assert declared_c_symbols() == sorted(rt4.C_EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(rt4):
+    L = rt4.lib()
+    for name in declared_c_symbols():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(rt4.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for name in list(rt4.C_EXPORTS) + list(rt4.CXX_EXPORTS):
+        assert name in exported, name
+    # nothing but the ABI and the reference-compatible prototypes leaks out
+    assert all(s.startswith("rt4_") or s.startswith("_Z") for s in exported)
+    assert all(s in rt4.CXX_EXPORTS for s in exported if s.startswith("_Z"))
+
+
+def test_abi_version(rt4):
+    assert rt4.lib().rt4_abi_version() == 1
+
+
+DUMMY = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("rows,N,K", [(5, 64, 256), (0, 64, 256), (4, 64, 200), (4, 0, 256)])
+def test_gemv_shape_errors(rt4, rows, N, K):
+    L = rt4.lib()
+    rc = L.rt4_gemv_w4a8(DUMMY, DUMMY, DUMMY, DUMMY, rows, N, K, None)
+    assert rc == 1  # RT4_E_SHAPE
+    assert "k_gemv_w4a8" in L.rt4_last_error().decode()
+    rc = L.rt4_gemv_w4a8_q(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, rows, N, K, None)
+    assert rc == 1
+
+
+def test_gemv_null_and_config_errors(rt4):
+    L = rt4.lib()
+    assert L.rt4_gemv_w4a8(None, DUMMY, DUMMY, DUMMY, 1, 64, 256, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 4, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 16, None) == 2
+    assert "config" in L.rt4_last_error().decode()
+
+
+def test_quant_errors(rt4):
+    L = rt4.lib()
+    assert L.rt4_quant_act_a8(DUMMY, DUMMY, None, DUMMY, 1, 100, None) == 1
+    assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 4, 256, 96, 0, 0, None) == 2
+    assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 4, 200, 128, 0, 0, None) == 2
+    assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 256, 128, 0, 0, None) == 1
+    assert L.rt4_quant_rows_i8(DUMMY, DUMMY, DUMMY, 4, 200, 0, 0, None) == 1
+    assert L.rt4_quant_rows_a4(DUMMY, DUMMY, DUMMY, 4, 256, 12, 0, 0, None) == 2
+
+
+def test_shim_exits_like_the_reference():
+    """k_gemv_w4a8 with rows > 4 prints and exits(1) (src/k_gemv.hip:54), via a C++ caller."""
+    src = ROOT / "tests" / "shim_caller.cpp"
+    exe = ROOT / "tests" / "_shim_caller"
+    lib = ROOT / "k100lc-rt4_amd" / "rt4_amd" / "lib"
+    subprocess.run(["g++", "-std=c++17", "-I", str(ROOT / "include"), str(src), "-L", str(lib),
+                    "-lrt4k", f"-Wl,-rpath,{lib}", "-o", str(exe)], check=True)
+    try:
+        r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    finally:
+        exe.unlink(missing_ok=True)
+    assert r.returncode == 1
+    assert "k_gemv_w4a8" in r.stdout and "rows=5" in r.stdout
