@@ -59,11 +59,12 @@ int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int ro
 int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                     const float* sa, int rows, int N, int K, void* stream);
 
-/* Same, with an explicit launch configuration (tuning and tests):
- * tiles = 16-row weight tiles per workgroup (1 or 2), waves = waves per
- * workgroup splitting K (1..16 for tiles=1, 1..8 for tiles=2). */
+/* Same, with an explicit launch configuration (tuning and tests).  A
+ * workgroup owns one 16-row weight tile; groups_per_wave (even, 2..12) is the
+ * number of 128-wide K groups each wave streams per pass, waves (1..16, at most
+ * the number of such chunks) the waves per workgroup.  0 selects the default. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
-                        const float* sa, int rows, int N, int K, int tiles, int waves,
+                        const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         void* stream);
 
 /* Test hook: the same kernel, also writing the exact per-group int32 dot
@@ -101,6 +102,32 @@ int rt4_quant_rows_i8(int8_t* xq, float* sc, const float* x, int rows, int K, in
 /* h/l digit planes -> interleaved int8 codes q8 = 16h + l. */
 int rt4_digits_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
                      void* stream);
+
+/* W4A8 prefill GEMM.  Replaces k_gemm_i4_a8 (src/kernels.h:32, src/k_gemm.hip:
+ * 22-34, kernel gemm_w4a4 of kernels/gemm_core.h:59-206 run twice plus
+ * k_add_inplace), with the same preconditions (M % 128, N % 64, K % 128 == 0)
+ * and arguments: c f32 [M][N] = Σ_g sb[g][n] * (sc16[g][m]*I_h + sc[g][m]*I_l)
+ * where I_h, I_l are the per-group int4 x int4 dots of the digit planes ah, al
+ * (uint32 [M][K/8], from rt4_quant_rows_a8) with wq.  Here the digits are
+ * recombined into q8 = 16h + l and contracted once, so each group's integer
+ * 16*I_h + I_l = Σ code*q8 is exact and scaled by sc[g][m]*wsc_gm[g][n]; sc16
+ * must be 16*sc as rt4_quant_rows_a8 writes it and is not read.  c2 (M*N
+ * floats, as in the reference) is scratch: it holds the recombined int8 codes
+ * when 4*N >= K, otherwise library scratch (grown with hipMalloc) is used. */
+int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, const uint32_t* ah,
+                  const uint32_t* al, const float* sc, const float* sc16, int M, int N, int K,
+                  void* stream);
+
+/* The same GEMM on int8 codes: xq int8 [M][K] interleaved (rt4_quant_rows_i8
+ * output), sc f32 [K/128][M].  No reference counterpart (it is k_gemm_i4_a8
+ * without the digit planes).  M >= 1, N >= 1, K % 128 == 0. */
+int rt4_gemm_w4a8_i8(float* c, const uint32_t* wq, const float* wsc_gm, const int8_t* xq,
+                     const float* sc, int M, int N, int K, void* stream);
+
+/* Test hook: rt4_gemm_w4a8_i8 that also writes the exact per-group int32 dot
+ * products gsum int32 [M][N][K/128] = Σ_{k∈g} q8[m][k]*code[n][k]. */
+int rt4_gemm_w4a8_groupsums(int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
+                            const int8_t* xq, const float* sc, int M, int N, int K, void* stream);
 
 /* RT4 fp16 row-major scales -> fp32 group-major.  Replaces the host helper
  * make_group_major (src/model.cpp:190-202), on the device. */

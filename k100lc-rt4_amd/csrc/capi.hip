@@ -67,10 +67,7 @@ int check_gemv_shape(const char* who, int rows, int N, int K) {
     if (rows < 1 || rows > 4) return fail(RT4_E_SHAPE, "%s: rows=%d not in [1,4] (prefill uses the GEMM)", who, rows);
     if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "%s: K=%d is not a positive multiple of 128", who, K);
     if (N <= 0) return fail(RT4_E_SHAPE, "%s: N=%d must be positive", who, N);
-    // the quantized activations of a call are staged whole in one workgroup's LDS
-    if ((size_t)rows * K > rt4::kGemvMaxActBytes)
-        return fail(RT4_E_SHAPE, "%s: rows*K=%lld exceeds the %d-byte activation stage", who,
-                    (long long)rows * K, (int)rt4::kGemvMaxActBytes);
+    if (N > 65535 * 16) return fail(RT4_E_SHAPE, "%s: N=%d too large", who, N);
     return RT4_OK;
 }
 
@@ -82,6 +79,23 @@ int check_gemv_align(const char* who, const void* y, const uint32_t* wq, const u
     if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
         return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
     return RT4_OK;
+}
+
+int check_gemm_args(const char* who, int M, int N, int K) {
+    if (M < 1 || N < 1) return fail(RT4_E_SHAPE, "%s: M=%d N=%d must be positive", who, M, N);
+    if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "%s: K=%d is not a positive multiple of 128", who, K);
+    if (M > 65535 * 128) return fail(RT4_E_SHAPE, "%s: M=%d too large", who, M);
+    return RT4_OK;
+}
+
+int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
+                   const int8_t* xq, const float* sc, int M, int N, int K, void* stream) {
+    if (!c || !wq || !wsc_gm || !xq || !sc) return fail(RT4_E_ARG, "%s: null pointer", who);
+    int rc = check_gemm_args(who, M, N, K);
+    if (rc) return rc;
+    if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(c, 4) || !aligned(sc, 4) || !aligned(wsc_gm, 4))
+        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
+    return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, as_stream(stream)), who);
 }
 
 }  // namespace
@@ -103,15 +117,20 @@ int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int ro
 }
 
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
-                        const float* sa, int rows, int N, int K, int tiles, int waves,
+                        const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         void* stream) {
     if (!y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8", rows, N, K);
     if (rc || (rc = check_gemv_align("rt4_gemv_w4a8", y, wq, ws, xq, sa))) return rc;
     rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
-    if (tiles > 0) c.rt = tiles;
+    if (groups_per_wave > 0) {
+        c.gpw = groups_per_wave;
+        const int nc = (K / 128 + c.gpw - 1) / c.gpw;
+        c.waves = nc < rt4::kGemvMaxWaves ? nc : rt4::kGemvMaxWaves;
+    }
     if (waves > 0) c.waves = waves;
-    if (!rt4::gemv_cfg_valid(c, K)) return fail(RT4_E_ARG, "rt4_gemv_w4a8: bad config tiles=%d waves=%d", c.rt, c.waves);
+    if (!rt4::gemv_cfg_valid(c, K))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a8: bad config groups_per_wave=%d waves=%d", c.gpw, c.waves);
     return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, xq, sa, rows, N, K, c, as_stream(stream)),
                       "rt4_gemv_w4a8 launch");
 }
@@ -194,6 +213,43 @@ int rt4_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, i
         return fail(RT4_E_SHAPE, "rt4_quant_rows_a4: rows=%d in_stride=%d in_off=%d", rows, in_stride, in_off);
     return hip_status(rt4::launch_quant_rows_a4(q, sc, x, rows, K, G, in_stride, in_off, as_stream(stream)),
                       "rt4_quant_rows_a4 launch");
+}
+
+
+int rt4_gemm_w4a8_i8(float* c, const uint32_t* wq, const float* wsc_gm, const int8_t* xq,
+                     const float* sc, int M, int N, int K, void* stream) {
+    return gemm_i8_common("rt4_gemm_w4a8_i8", nullptr, c, wq, wsc_gm, xq, sc, M, N, K, stream);
+}
+
+int rt4_gemm_w4a8_groupsums(int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
+                            const int8_t* xq, const float* sc, int M, int N, int K, void* stream) {
+    if (!gsum) return fail(RT4_E_ARG, "rt4_gemm_w4a8_groupsums: null pointer");
+    return gemm_i8_common("rt4_gemm_w4a8_groupsums", gsum, c, wq, wsc_gm, xq, sc, M, N, K, stream);
+}
+
+int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, const uint32_t* ah,
+                  const uint32_t* al, const float* sc, const float* sc16, int M, int N, int K,
+                  void* stream) {
+    if (!c || !c2 || !wq || !wsc_gm || !ah || !al || !sc || !sc16)
+        return fail(RT4_E_ARG, "k_gemm_i4_a8: null pointer");
+    // the reference's tile preconditions (src/k_gemm.hip:24-28)
+    if (M <= 0 || N <= 0 || K <= 0 || M % 128 || N % 64 || K % 128)
+        return fail(RT4_E_SHAPE, "k_gemm_i4_a8: shape must be multiples of BM=128/BN=64/G=128 (M=%d N=%d K=%d)",
+                    M, N, K);
+    int rc = check_gemm_args("k_gemm_i4_a8", M, N, K);
+    if (rc) return rc;
+    if (!aligned(ah, 4) || !aligned(al, 4) || !aligned(c2, 16))
+        return fail(RT4_E_ARG, "k_gemm_i4_a8: misaligned pointer");
+    // Recombine the digit planes into int8 codes q8 = 16h + l.  The caller's c2
+    // (M*N floats of scratch, src/k_gemm.hip:31) holds them when large enough.
+    const size_t need = (size_t)M * K;
+    void* q = c2;
+    if ((size_t)M * N * sizeof(float) < need && (rc = scratch(kSlotGemmA, need, &q))) return rc;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st);
+    if (e != hipSuccess) return hip_status(e, "k_gemm_i4_a8 digit recombination");
+    return hip_status(rt4::launch_gemm_w4a8(c, nullptr, static_cast<const int8_t*>(q), wq, sc, wsc_gm, M, N, K, st),
+                      "k_gemm_i4_a8 launch");
 }
 
 int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream) {

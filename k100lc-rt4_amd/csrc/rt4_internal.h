@@ -22,16 +22,21 @@ hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG
 
 // ---- decode GEMV (gemv.hip)
 struct GemvCfg {
-    int rt;     // 16-row weight tiles per workgroup (1 or 2)
-    int waves;  // waves per workgroup; they split the K groups of the tile
+    int gpw;    // K groups per wave (even, 2..12)
+    int waves;  // waves per workgroup; they share one 16-row tile and split its K groups
 };
-constexpr int kGemvMaxGroupsPerWave = 10;  // weight loads one wave keeps in flight
 constexpr int kGemvMaxWaves = 16;
-constexpr size_t kGemvMaxActBytes = 160 * 1024;  // rows*K int8 staged in one workgroup's LDS
 GemvCfg gemv_default_cfg(int rows, int N, int K);
 bool gemv_cfg_valid(const GemvCfg& c, int K);
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,
                             const int8_t* xq, const float* sa, int rows, int N, int K,
                             const GemvCfg& cfg, hipStream_t st);
+
+// ---- prefill GEMM (gemm.hip)
+// C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],
+// group-major scales sa [K/128][M] and sb [K/128][N]; gsum (optional, tests)
+// receives the exact per-group int32 dot products [M][N][K/128].
+hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint32_t* W,
+                            const float* sa, const float* sb, int M, int N, int K, hipStream_t st);
 
 }  // namespace rt4

@@ -34,3 +34,10 @@ void k_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int
     if (rt4_quant_rows_a4(q, sc, x, rows, K, G, in_stride, in_off, nullptr) != RT4_OK)
         die("k_quant_rows");
 }
+
+// src/k_gemm.hip:22-34
+void k_gemm_i4_a8(float* c, float* c2, const u32* wq, const float* wsc_gm, const u32* ah,
+                  const u32* al, const float* sc, const float* sc16, int M, int N, int K) {
+    if (rt4_gemm_w4a8(c, c2, wq, wsc_gm, ah, al, sc, sc16, M, N, K, nullptr) != RT4_OK)
+        die("k_gemm_i4_a8");
+}

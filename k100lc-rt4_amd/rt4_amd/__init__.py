@@ -28,12 +28,14 @@ C_EXPORTS = (
     "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_w4a8_groupsums",
     "rt4_gemv_w4a8", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
     "rt4_make_group_major", "rt4_quant_rows_a4",
+    "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
 )
 # The reference-compatible C++ entry points (include/rt4_kernels.h), mangled.
 CXX_EXPORTS = (
     "_Z11k_gemv_w4a8PfPKjPKfS3_iii",
     "_Z15k_quant_rows_a8PjS_PfS0_PKfiiiii",
     "_Z12k_quant_rowsPjPfPKfiiiii",
+    "_Z12k_gemm_i4_a8PfS_PKjPKfS1_S1_S3_S3_iii",
 )
 
 
@@ -55,16 +57,31 @@ _SIGS = {
     "rt4_digits_to_i8": [_P, _P, _P, _I, _I, _P],
     "rt4_make_group_major": [_P, _P, _I, _I, _P],
     "rt4_quant_rows_a4": [_P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "rt4_gemm_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemm_w4a8_i8": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemm_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
 }
 
 
 def lib() -> ctypes.CDLL:
-    """Load librt4k.so once (no GPU work happens at load time)."""
+    """Load librt4k.so once (no GPU work happens at load time).
+
+    torch wheels bundle their own HIP runtime whose soname (libamdhip64.so.7)
+    equals the system one librt4k.so links.  Importing torch first lets the
+    dynamic linker bind librt4k.so to that already loaded runtime, so the
+    process holds a single HIP/HSA runtime; loading librt4k.so first would pull
+    in /opt/rocm's copy as well, and whichever of the two initialises second
+    finds no device.
+    """
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             raise RT4Error(f"{LIB_PATH} is missing: build it with `make -C k100lc-rt4_amd` "
                            "or __graft_entry__.build()")
+        try:
+            import torch  # noqa: F401  (see the docstring: one HIP runtime per process)
+        except ImportError:
+            pass
         L = ctypes.CDLL(str(LIB_PATH))
         L.rt4_last_error.restype = ctypes.c_char_p
         L.rt4_last_error.argtypes = []
@@ -118,14 +135,14 @@ def quant_act_a8(x, want_sums: bool = False):
     return (xq, sa, asu) if want_sums else (xq, sa)
 
 
-def gemv_w4a8_q(wq, ws, xq, sa, out=None, tiles: int = 0, waves: int = 0):
+def gemv_w4a8_q(wq, ws, xq, sa, out=None, groups_per_wave: int = 0, waves: int = 0):
     """W4A8 GEMV on quantized activations.  wq int32/uint32 [N, K/8], ws int16/fp16 [N, K/128]."""
     torch = _torch()
     rows, K = xq.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, xq.device)
     _check(lib().rt4_gemv_w4a8_q_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(xq), _ptr(sa), rows, N, K,
-                                     tiles, waves, _stream()))
+                                     groups_per_wave, waves, _stream()))
     return y
 
 
@@ -206,3 +223,39 @@ def quant_rows_a4(x, rows: int | None = None, K: int | None = None, G: int = GRO
     _check(lib().rt4_quant_rows_a4(_ptr(q), _ptr(sc), _ptr(x), rows, K, G, in_stride, in_off,
                                    _stream()))
     return q, sc
+
+
+def gemm_w4a8_i8(wq, wsc_gm, xq, sc, out=None):
+    """Prefill GEMM on int8 codes: xq int8 [M, K] interleaved, sc f32 [K/128, M],
+    wq int32 [N, K/8], wsc_gm f32 [K/128, N] -> c f32 [M, N]."""
+    torch = _torch()
+    M, K = xq.shape
+    N = wq.shape[0]
+    c = out if out is not None else _empty((M, N), torch.float32, xq.device)
+    _check(lib().rt4_gemm_w4a8_i8(_ptr(c), _ptr(wq), _ptr(wsc_gm), _ptr(xq), _ptr(sc), M, N, K, _stream()))
+    return c
+
+
+def gemm_w4a8_groupsums(wq, wsc_gm, xq, sc):
+    """Same kernel, returning (c, gsum int32 [M, N, K/128]) -- small shapes only."""
+    torch = _torch()
+    M, K = xq.shape
+    N = wq.shape[0]
+    c = _empty((M, N), torch.float32, xq.device)
+    gs = _empty((M, N, K // GROUP), torch.int32, xq.device)
+    _check(lib().rt4_gemm_w4a8_groupsums(_ptr(gs), _ptr(c), _ptr(wq), _ptr(wsc_gm), _ptr(xq), _ptr(sc),
+                                         M, N, K, _stream()))
+    return c, gs
+
+
+def gemm_w4a8(wq, wsc_gm, qh, ql, sc, sc16, out=None, c2=None):
+    """Drop-in k_gemm_i4_a8 on the digit planes of quant_rows_a8 -> c f32 [M, N]."""
+    torch = _torch()
+    M, KD = qh.shape
+    K = KD * 8
+    N = wq.shape[0]
+    c = out if out is not None else _empty((M, N), torch.float32, qh.device)
+    c2 = c2 if c2 is not None else _empty((M, N), torch.float32, qh.device)
+    _check(lib().rt4_gemm_w4a8(_ptr(c), _ptr(c2), _ptr(wq), _ptr(wsc_gm), _ptr(qh), _ptr(ql), _ptr(sc),
+                               _ptr(sc16), M, N, K, _stream()))
+    return c

@@ -1,38 +1,29 @@
-// ref_bind.hip -- C-callable handles onto the reference's own hot-path kernels,
-// compiled in place from /root/reference for gfx950 by oracle/Makefile into
-// oracle/_ref/libref_hip.so.
+// ref_bind.hip -- C-callable handles onto the reference's own activation
+// quantizer kernels, compiled in place from /root/reference for gfx950 by
+// oracle/Makefile into oracle/_ref/libref_hip.so.
 //
-// TEST INFRASTRUCTURE ONLY: used by tests/ to pin the CPU oracle (and our HIP
-// kernels) against the reference implementation on the same seeded inputs.
-// Nothing in the product library links this.
+// TEST INFRASTRUCTURE ONLY: used by tests/ as a third-party check of the CPU
+// oracle (and of our HIP quantizers) on the same seeded inputs.  Nothing in the
+// product library links this.
 //
-// The reference's GEMV wrapper keeps its quantized activations in file-static
-// scratch (src/k_gemv.hip:47-51); this TU compiles that file as part of itself so
-// the codes it produced can be read back for a bit-exact comparison.
-#include "../src/k_gemv.hip"  // resolved through -I<reference>/kernels
+// Only the quantizers are bound.  They are plain C++ float/integer code, so
+// their gfx950 build computes what the gfx926 build does.  The reference's
+// GEMV/GEMM kernels are deliberately left out: their dot products are inline
+// assembly (v_dot4_i32_i8, kernels/gemv_w4a8_core.h:25-29; v_dot8_i32_i4,
+// kernels/gemm_core.h:167) written for gfx926, and a gfx950 build of
+// k_gemv_w4a8 was observed to return outputs ~4e5x off while the quantizer
+// output of the same call was bit-exact -- so they are not the reference's
+// arithmetic on this target and are never run.
+#include "gemv_w4a8_core.h"  // quant_act (kernels/gemv_w4a8_core.h:34-66); resolved via -I<reference>/kernels
+#include "kernels.h"         // k_quant_rows_a8 / k_quant_rows (src/k_new.hip), -I<reference>/src
 
 extern "C" {
 
-// k_gemv_w4a8, src/k_gemv.hip:53-106 (null stream; exits on shape errors).
-void ref_gemv_w4a8(float* y, const u32* wq, const uint16_t* ws, const float* x, int rows, int N,
-                   int K) {
-    k_gemv_w4a8(y, wq, (const float*)ws, x, rows, N, K);
-}
-
-// Read back the activation quantization of the last ref_gemv_w4a8 call:
-// even/odd int8 halves [rows][K/2], scales and sums [rows][K/128].
-void ref_gemv_last_quant(int8_t* ae, int8_t* ao, float* asc, int* asu, int rows, int K) {
-    hipDeviceSynchronize();
-    hipMemcpy(ae, s_ae, (size_t)rows * (K / 2), hipMemcpyDeviceToHost);
-    hipMemcpy(ao, s_ao, (size_t)rows * (K / 2), hipMemcpyDeviceToHost);
-    hipMemcpy(asc, s_asc, (size_t)rows * (K / GRP) * 4, hipMemcpyDeviceToHost);
-    hipMemcpy(asu, s_asu, (size_t)rows * (K / GRP) * 4, hipMemcpyDeviceToHost);
-}
-
-// k_gemv_w4a4, src/k_gemv.hip:14-42.
-void ref_gemv_w4a4(float* y, const u32* wq, const uint16_t* ws, const float* x, int rows, int N,
-                   int K) {
-    k_gemv_w4a4(y, wq, (const float*)ws, x, rows, N, K);
+// quant_act, kernels/gemv_w4a8_core.h:34-66, launched as src/k_gemv.hip:70 does:
+// grid (K/128, rows) x 32 threads.  Outputs the even/odd int8 halves
+// [rows][K/2], scales and sums [rows][K/128] into caller device buffers.
+void ref_quant_act(const float* x, int8_t* ae, int8_t* ao, float* asc, int* asu, int rows, int K) {
+    quant_act<<<dim3(K / GRP, rows), 32>>>(x, ae, ao, asc, asu, rows, K);
 }
 
 // k_quant_rows_a8, src/k_new.hip:296-301.
@@ -45,18 +36,6 @@ void ref_quant_rows_a8(u32* qh, u32* ql, float* sc, float* sc16, const float* x,
 void ref_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int in_stride,
                     int in_off) {
     k_quant_rows(q, sc, x, rows, K, G, in_stride, in_off);
-}
-
-// k_gemm_i4_a8, src/k_gemm.hip:22-34.
-void ref_gemm_i4_a8(float* c, float* c2, const u32* wq, const float* wsc_gm, const u32* ah,
-                    const u32* al, const float* sc, const float* sc16, int M, int N, int K) {
-    k_gemm_i4_a8(c, c2, wq, wsc_gm, ah, al, sc, sc16, M, N, K);
-}
-
-// k_gemm_i4, src/k_gemm.hip:8-17.
-void ref_gemm_i4(float* c, const u32* wq, const float* wsc_gm, const u32* aq, const float* asc_gm,
-                 int M, int N, int K) {
-    k_gemm_i4(c, wq, wsc_gm, aq, asc_gm, M, N, K);
 }
 
 void ref_sync(void) { hipDeviceSynchronize(); }

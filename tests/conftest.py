@@ -46,20 +46,16 @@ def torch_gpu():
 
 @pytest.fixture(scope="session")
 def ref_hip(torch_gpu):
-    """The reference's own kernels built for gfx950 (oracle/_ref), if present."""
+    """The reference's own activation quantizers built for gfx950 (oracle/_ref), if present."""
     if not REF_HIP.exists():
         pytest.skip("oracle/_ref/libref_hip.so not built (needs /root/reference at build time)")
     L = ctypes.CDLL(str(REF_HIP))
     P, I = ctypes.c_void_p, ctypes.c_int
-    L.ref_gemv_w4a8.argtypes = [P, P, P, P, I, I, I]
-    L.ref_gemv_last_quant.argtypes = [P, P, P, P, I, I]
-    L.ref_gemv_w4a4.argtypes = [P, P, P, P, I, I, I]
+    L.ref_quant_act.argtypes = [P, P, P, P, P, I, I]
     L.ref_quant_rows_a8.argtypes = [P, P, P, P, P, I, I, I, I, I]
     L.ref_quant_rows.argtypes = [P, P, P, I, I, I, I, I]
-    L.ref_gemm_i4_a8.argtypes = [P, P, P, P, P, P, P, P, I, I, I]
-    L.ref_gemm_i4.argtypes = [P, P, P, P, P, I, I, I]
-    for f in ("ref_gemv_w4a8", "ref_gemv_last_quant", "ref_gemv_w4a4", "ref_quant_rows_a8",
-              "ref_quant_rows", "ref_gemm_i4_a8", "ref_gemm_i4", "ref_sync"):
+    L.ref_sync.argtypes = []
+    for f in ("ref_quant_act", "ref_quant_rows_a8", "ref_quant_rows", "ref_sync"):
         getattr(L, f).restype = None
     return L
 

@@ -59,8 +59,9 @@ def test_gemv_shape_errors(rt4, rows, N, K):
 def test_gemv_null_and_config_errors(rt4):
     L = rt4.lib()
     assert L.rt4_gemv_w4a8(None, DUMMY, DUMMY, DUMMY, 1, 64, 256, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 4, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 16, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 1, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 2, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 14, 1, None) == 2
     assert "config" in L.rt4_last_error().decode()
 
 
@@ -87,3 +88,11 @@ def test_shim_exits_like_the_reference():
         exe.unlink(missing_ok=True)
     assert r.returncode == 1
     assert "k_gemv_w4a8" in r.stdout and "rows=5" in r.stdout
+
+
+def test_single_hip_runtime_in_process(rt4):
+    """librt4k.so binds to the HIP runtime torch already loaded (one runtime per process)."""
+    import torch  # noqa: F401
+    rt4.lib()
+    maps = {line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line}
+    assert len(maps) == 1, maps
