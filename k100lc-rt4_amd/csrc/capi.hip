@@ -31,7 +31,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // hipFree synchronizes the device, so a buffer still read by queued kernels is
 // never released early.  Not safe for concurrent calls from several threads
 // (the reference's scratch has the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlots = 3 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlots = 5 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -40,7 +40,7 @@ struct Buf {
 std::mutex g_mu;
 Buf g_buf[kMaxDev][kSlots];
 
-int scratch(Slot slot, size_t bytes, void** out) {
+int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, bool zero = false) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
@@ -58,6 +58,10 @@ int scratch(Slot slot, size_t bytes, void** out) {
         e = hipMalloc(&b.p, want);
         if (e != hipSuccess) return hip_status(e, "hipMalloc(scratch)");
         b.cap = want;
+        if (zero) {
+            e = rt4::launch_zero_i32(static_cast<int*>(b.p), want / sizeof(int), zero_on);
+            if (e != hipSuccess) return hip_status(e, "zeroing scratch");
+        }
     }
     *out = b.p;
     return RT4_OK;
@@ -88,6 +92,36 @@ int check_gemm_args(const char* who, int M, int N, int K) {
     return RT4_OK;
 }
 
+int device_cus(int* cus) {
+    static int cache[kMaxDev] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDev) return fail(RT4_E_ARG, "device %d out of range", dev);
+    if (!cache[dev]) {
+        int v = 0;
+        e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return hip_status(e, "hipDeviceGetAttribute");
+        cache[dev] = v > 0 ? v : 256;
+    }
+    *cus = cache[dev];
+    return RT4_OK;
+}
+
+// The GEMM launch with its library-owned split-tile workspace.
+int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
+             const int8_t* xq, const float* sc, int M, int N, int K, hipStream_t st) {
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    const rt4::GemmPlan plan = rt4::gemm_plan(M, N, K, cus);
+    void *part = nullptr, *cnt = nullptr;
+    if ((rc = scratch(kSlotGemmPart, plan.part_bytes, &part))) return rc;
+    if ((rc = scratch(kSlotGemmCnt, plan.cnt_bytes, &cnt, st, true))) return rc;
+    return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, plan, static_cast<float*>(part),
+                                            static_cast<int*>(cnt), st),
+                      who);
+}
+
 int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
                    const int8_t* xq, const float* sc, int M, int N, int K, void* stream) {
     if (!c || !wq || !wsc_gm || !xq || !sc) return fail(RT4_E_ARG, "%s: null pointer", who);
@@ -95,7 +129,7 @@ int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq,
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(c, 4) || !aligned(sc, 4) || !aligned(wsc_gm, 4))
         return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
-    return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, as_stream(stream)), who);
+    return run_gemm(who, gsum, c, wq, wsc_gm, xq, sc, M, N, K, as_stream(stream));
 }
 
 }  // namespace
@@ -248,8 +282,7 @@ int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, 
     hipStream_t st = as_stream(stream);
     hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4_a8 digit recombination");
-    return hip_status(rt4::launch_gemm_w4a8(c, nullptr, static_cast<const int8_t*>(q), wq, sc, wsc_gm, M, N, K, st),
-                      "k_gemm_i4_a8 launch");
+    return run_gemm("k_gemm_i4_a8 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), sc, M, N, K, st);
 }
 
 int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream) {

@@ -35,8 +35,20 @@ hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const u
 // ---- prefill GEMM (gemm.hip)
 // C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],
 // group-major scales sa [K/128][M] and sb [K/128][N]; gsum (optional, tests)
-// receives the exact per-group int32 dot products [M][N][K/128].
+// receives the exact per-group int32 dot products [M][N][K/128].  The launch is
+// persistent (one workgroup per CU, equal shares of the (tile, group) units);
+// `part` and `cnt` are its split-tile workspace: part_bytes of partial sums and
+// cnt_bytes of counters that must be zero before the first launch (every launch
+// leaves them zero again).
+struct GemmPlan {
+    int ntm, ntn, ntiles, P;
+    long long T;
+    size_t part_bytes, cnt_bytes;
+};
+GemmPlan gemm_plan(int M, int N, int K, int cus);
 hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint32_t* W,
-                            const float* sa, const float* sb, int M, int N, int K, hipStream_t st);
+                            const float* sa, const float* sb, int M, int N, int K, const GemmPlan& plan,
+                            float* part, int* cnt, hipStream_t st);
+hipError_t launch_zero_i32(int* p, size_t n, hipStream_t st);
 
 }  // namespace rt4
