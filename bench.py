@@ -57,17 +57,24 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-kernel table beyond the roofline")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="only launch the dominant kernels and a calibration copy, eagerly (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
-def timed_graph(torch, fn, reps: int = 5) -> float:
-    """Capture fn() in a HIP graph, replay it, return ms per replay (median of reps)."""
+def timed_graph(torch, fn, reps: int = 5, warm_ms: float = 50.0) -> float:
+    """Capture fn() in a HIP graph, replay it, return ms per replay (median of reps).
+    Replays for at least warm_ms first: the GPU clock needs tens of milliseconds of
+    load to settle, and a cold first measurement reads ~10% slow."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         fn()
-    g.replay()
-    g.replay()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while True:
+        g.replay()
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= warm_ms:
+            break
     times = []
     for _ in range(reps):
         a = torch.cuda.Event(enable_timing=True)
@@ -177,6 +184,53 @@ def gemm_table(torch, rt4_amd, workload, gen) -> dict:
     return out
 
 
+def load_traffic(key: str):
+    """Bytes per launch of `key` measured by the FETCH_SIZE / WRITE_SIZE counter runs
+    (rt4_amd.profiling), or None when that summary is absent."""
+    try:
+        d = json.loads((ROOT / "profiles" / "traffic.json").read_text())[key]
+        return int(d["traffic_bytes"])
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+def pmc_probe(torch, rt4_amd, workload, gen) -> int:
+    """Eager launches for counter collection: the gate/up GEMV over 16 distinct weight
+    sets (twice), the gate/up prefill GEMM 3 times, and 4 copies of COPY_BYTES."""
+    import ctypes
+
+    from rt4_amd import probe, profiling
+    M, (N, K) = 4, (17408, 5120)
+    mats = [workload.weights_torch(N, K, generator=gen) for _ in range(16)]
+    x = workload.acts_torch(M, K, generator=gen)
+    xq, sa = rt4_amd.quant_act_a8(x)
+    y = torch.empty((M, N), device="cuda")
+    for _ in range(2):
+        for wq, ws in mats:
+            rt4_amd.gemv_w4a8_q(wq, ws, xq, sa, out=y)
+    del mats
+    Mg, Ng, Kg = workload.GEMM_SHAPES["c2_gate_up"]
+    wq, ws = workload.weights_torch(Ng, Kg, generator=gen)
+    sb = rt4_amd.make_group_major(ws, Kg)
+    xg = workload.acts_torch(Mg, Kg, outliers=True, generator=gen)
+    xq8, sc = rt4_amd.quant_rows_i8(xg)
+    c = torch.empty((Mg, Ng), device="cuda")
+    for _ in range(3):
+        rt4_amd.gemm_w4a8_i8(wq, sb, xq8, sc, out=c)
+    nb = profiling.COPY_BYTES
+    src = torch.empty(nb // 4, dtype=torch.int32, device="cuda").random_()
+    dst = torch.empty_like(src)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for _ in range(4):
+        rc = probe.lib().rt4p_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()), nb, cus * 8, st)
+        if rc:
+            raise RuntimeError(f"rt4p_copy failed ({rc})")
+    torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -193,6 +247,8 @@ def main() -> int:
     metric = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
     torch.cuda.set_device(0)
     gen = torch.Generator(device="cuda").manual_seed(0)
+    if args.pmc_probe:
+        return pmc_probe(torch, rt4_amd, workload, gen)
     M = 4
     (Ngu, Kgu), (Nd, Kd) = (17408, 5120), (5120, 17408)
     L = max(1, args.layers)
@@ -258,7 +314,7 @@ def main() -> int:
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     roofline = {"kernel": "rt4::gemv_w4a8_k<4,10,false> (gate/up, M=4 K=5120 N=17408)",
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv_gate_up"),
                 "us_per_launch": round(gu_us, 3), "bytes_per_launch": gu_bytes,
                 "weight_only_GBs": round((Ngu * Kgu // 2) / (gu_us * 1e-6) / 1e9, 1)}
 

@@ -23,12 +23,25 @@
 //
 // Data movement.  Per group the workgroup moves 16 KB of int8 activations, 16 KB
 // of packed weights and the two scale vectors from global memory straight into
-// LDS with global_load_lds_dwordx4 (no VGPR round trip), four stages deep, XOR-
-// swizzled so the MFMA fragment reads are bank-conflict free; the weights stay
-// packed in LDS and are unpacked after the ds_read.  The LDS DMA is issued from
-// inline asm so the compiler does not serialise every LDS read behind all
-// outstanding DMA; the kernel waits for the stage it reads (s_waitcnt vmcnt +
-// barrier) itself.
+// LDS with global_load_lds_dwordx4 (no VGPR round trip): four A+B stages and a
+// ring of five scale slots, so unit i+4 is loading while unit i computes.  The
+// LDS layouts are XOR-swizzled for gfx950's 64-bank LDS, which serves 16 lanes
+// of a ds_read_b128 per cycle: any 16 consecutive fragment rows hit 16 distinct
+// 16-byte bank groups.  The weights stay packed in LDS and are unpacked after
+// the ds_read.  The DMA is issued from inline asm with a per-lane 32-bit offset
+// (fixed while the tile is unchanged) and a scalar 64-bit base (advanced per
+// group), so it costs no vector ALU work; the compiler does not see it, so it
+// does not serialise LDS reads behind it -- the kernel waits itself (s_waitcnt
+// vmcnt + barrier).
+//
+// Per unit each wave: unpacks the weight fragments of the unit (read during the
+// previous unit), reads its second activation fragment, runs tiles (0,0) and
+// (0,1), folds (0,0), passes the one barrier of the unit (DMA of unit i+1 landed,
+// stage i free), issues the DMA of unit i+4 into stage i, reads the fragments of
+// unit i+1, and runs tiles (1,0), (1,1) with the remaining folds in between.
+// The fold (cvt + mul + fma per output per group) is most of the vector ALU
+// work, and on gfx950 vector ALU and MFMA issue overlap only a little, so the
+// kernel is bound by VALU + MFMA issue rather than by memory.
 //
 // Scheduling ("stream-K").  With 128 x 256 tiles the 27B shapes give 544 or 160
 // tiles for 256 CUs, so a plain one-tile-per-workgroup grid would leave up to
@@ -43,7 +56,6 @@
 #include "rt4_internal.h"
 
 namespace rt4 {
-
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -54,7 +66,8 @@ constexpr int NT = 512;           // 8 waves
 constexpr int A_ST = BM * 128;    // int8 activation tile per stage
 constexpr int B_ST = BN * 64;     // packed weight tile per stage
 constexpr int S_ST = 2048;        // sa (512 B) + sb (1024 B) + 512 B of the idle waves' loads
-constexpr int STAGE = A_ST + B_ST + S_ST;
+constexpr int AB_ST = A_ST + B_ST;    // one A+B stage
+constexpr int NSC = 5;                // scale slots (a ring: unit i+4 is loaded while unit i folds)
 constexpr int DMA_PER_UNIT = 5;   // DMA instructions per wave per (tile, group) unit
 constexpr int PART_FLOATS = NT * 64;   // one partial tile: 64 outputs per thread, [k][thread]
 
@@ -140,49 +153,70 @@ __device__ __forceinline__ Unit unit_of(int u, int NG, int ntm) {
 
 // The DMA of one unit: per wave 2 A instructions (8 rows x 128 B each), 2 B
 // instructions (16 rows x 64 B each) and 1 scale instruction.  LDS layouts:
-//   A  [128 rows][8 x 16 B], 16-byte chunk c of row r stored at c ^ (r & 7)
-//   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 1) & 3)
+//   A  [128 rows][8 x 16 B], 16-byte chunk c of row r stored at c ^ ((r >> 1) & 7)
+//   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3)
 //   S  sa[128] f32, sb[256] f32
-__device__ __forceinline__ void issue(unsigned char* st, const int8_t* __restrict__ A,
-                                      const uint32_t* __restrict__ W, const float* __restrict__ sa,
-                                      const float* __restrict__ sb, int M, int N, int K, const Unit& x,
-                                      int w, int lane) {
+// Per-lane byte offsets of this wave's DMA sources within one (tile, group) unit,
+// relative to the unit's scalar bases; they change only when the tile changes.
+struct DmaOff {
+    uint32_t a[2], b[2], s;
+};
+__device__ __forceinline__ DmaOff dma_offsets(const Unit& x, int M, int N, int K, int w, int lane) {
+    DmaOff o;
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int i = 2 * w + t;
         const int r = 8 * i + (lane >> 3);
-        const int c = (lane & 7) ^ (r & 7);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
         int gr = x.bm() + r;
         gr = gr < M ? gr : M - 1;
-        dma16(A + (size_t)gr * K + (size_t)x.g * 128 + c * 16, st + i * 1024);
+        o.a[t] = (uint32_t)gr * (uint32_t)K + c * 16;
     }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int i = 2 * w + t;
         const int r = 16 * i + (lane >> 2);
-        const int c = (lane & 3) ^ ((r >> 1) & 3);
+        const int c = (lane & 3) ^ ((r >> 2) & 3);
         int gr = x.bn() + r;
         gr = gr < N ? gr : N - 1;
-        dma16(reinterpret_cast<const unsigned char*>(W) + (size_t)gr * (K >> 1) + (size_t)x.g * 64 + c * 16,
-              st + A_ST + i * 1024);
+        o.b[t] = (uint32_t)gr * (uint32_t)(K >> 1) + c * 16;
     }
-    unsigned char* sdst = st + A_ST + B_ST;
     if (w < 2) {
         int r = x.bm() + w * 64 + lane;
-        r = r < M ? r : M - 1;
-        dma4(sa + (size_t)x.g * M + r, sdst + w * 256);
+        o.s = (uint32_t)(r < M ? r : M - 1) * 4u;
     } else {
-        const int ww = (w - 2) & 3;   // waves 6, 7 repeat waves 2, 3 into the slack area
-        int r = x.bn() + ww * 64 + lane;
-        r = r < N ? r : N - 1;
-        dma4(sb + (size_t)x.g * N + r, sdst + 512 + (w < 6 ? 0 : 1024) + ww * 256);
+        int r = x.bn() + ((w - 2) & 3) * 64 + lane;
+        o.s = (uint32_t)(r < N ? r : N - 1) * 4u;
     }
+    return o;
+}
+__device__ __forceinline__ void dma16s(uint32_t voff, const void* base, unsigned char* l) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_addr(l)) : "memory");
+}
+__device__ __forceinline__ void dma4s(uint32_t voff, const void* base, unsigned char* l) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds_addr(l)) : "memory");
+}
+__device__ __forceinline__ void issue(unsigned char* st, unsigned char* sdst, const int8_t* __restrict__ A,
+                                      const uint32_t* __restrict__ W, const float* __restrict__ sa,
+                                      const float* __restrict__ sb, int M, int N, int K, const Unit& x,
+                                      const DmaOff& o, int w) {
+    const int8_t* ab = A + (size_t)x.g * 128;
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(W) + (size_t)x.g * 64;
+    dma16s(o.a[0], ab, st + (2 * w) * 1024);
+    dma16s(o.a[1], ab, st + (2 * w + 1) * 1024);
+    dma16s(o.b[0], wb, st + A_ST + (2 * w) * 1024);
+    dma16s(o.b[1], wb, st + A_ST + (2 * w + 1) * 1024);
+    if (w < 2)
+        dma4s(o.s, sa + (size_t)x.g * M, sdst + w * 256);
+    else
+        dma4s(o.s, sb + (size_t)x.g * N, sdst + 512 + (w < 6 ? 0 : 1024) + ((w - 2) & 3) * 256);
 }
 
 // Which workgroup's share contains unit u (shares are [T*b/P, T*(b+1)/P)).
 __device__ __forceinline__ int owner_of(long long u, long long T, int P) {
     return (int)(((u + 1) * P - 1) / T);
 }
+
 
 template <bool GSUM>
 __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ A,
@@ -194,19 +228,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
                                                      float* __restrict__ part,
                                                      int* __restrict__ cnt, int M, int N, int K,
                                                      int ntm, long long T) {
-    __shared__ __align__(16) unsigned char st0[STAGE];
-    __shared__ __align__(16) unsigned char st1[STAGE];
-    __shared__ __align__(16) unsigned char st2[STAGE];
-    __shared__ __align__(16) unsigned char st3[STAGE];
+    __shared__ __align__(16) unsigned char sab[4 * AB_ST];
+    __shared__ __align__(16) unsigned char ssc[NSC * S_ST];
     __shared__ int s_flag;
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6);
     const int wm = w & 1, wn = w >> 1;
     const int lr = lane & 31, lh = lane >> 5;
     const int NG = K >> 7;
-    // Workgroups are dispatched to the 8 XCDs round-robin; renumber them so each
-    // XCD owns one contiguous eighth of the units (its tiles share weight rows in
-    // its own L2).  All share bookkeeping below uses this logical index.
     const int P = gridDim.x;
     const int b = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const long long u0 = T * b / P, u1 = T * (b + 1) / P;
@@ -219,188 +248,195 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) facc[i][j][r] = 0;  // bits of +0.0f
+            for (int r = 0; r < 16; r++) facc[i][j][r] = 0;
 
-    // two cursors: `cu` = unit being computed, `iu` = unit being loaded (3 ahead,
-    // clamped to the last unit, whose loads are then simply repeated)
-    Unit cu = unit_of((int)u0, NG, ntm);
-    Unit iu = cu;
-    issue(st0, A, W, sa, sb, M, N, K, iu, w, lane);
-    if (1 < n) iu.next(NG, ntm);
-    issue(st1, A, W, sa, sb, M, N, K, iu, w, lane);
-    if (2 < n) iu.next(NG, ntm);
-    issue(st2, A, W, sa, sb, M, N, K, iu, w, lane);
-    const v16i zero16 = {};
-
-    for (int i4 = 0; i4 < n; i4 += 4) {
+    auto stage = [&](int i) { return sab + (i & 3) * AB_ST; };
+    auto slot = [&](int i) { return ssc + (i % NSC) * S_ST; };
+    auto read_a = [&](v4i (&dst)[4], const unsigned char* stg, int ii) {
+        const int r = 64 * wm + 32 * ii + lr;
 #pragma unroll
-        for (int sub = 0; sub < 4; sub++) {
-            const int i = i4 + sub;
-            if (i >= n) break;
-            // the DMA of unit i has landed once at most the 3 younger units' loads are pending
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
-            __syncthreads();
-            if (i + 3 < n) iu.next(NG, ntm);
-            issue(sub == 0 ? st3 : sub == 1 ? st0 : sub == 2 ? st1 : st2, A, W, sa, sb, M, N, K, iu, w, lane);
-            const unsigned char* cur = sub == 0 ? st0 : sub == 1 ? st1 : sub == 2 ? st2 : st3;
-            const Unit x = cu;
-            cu.next(NG, ntm);
-
-            // --- group dot products: k-step ks = 2s+t, lane half lh covers codes
-            //     [64s + 32lh + 16t, +16) of the group; one b128 of packed B per s
-            v16i acc[2][2];
+        for (int ks = 0; ks < 4; ks++) {
+            const int c = (4 * (ks >> 1) + 2 * lh + (ks & 1)) ^ ((r >> 1) & 7);
+            dst[ks] = *reinterpret_cast<const v4i*>(stg + r * 128 + c * 16);
+        }
+    };
+    auto read_b = [&](uint4 (&dst)[2][2], const unsigned char* stg) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                uint4 bp[2];
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const int r = 64 * wn + 32 * j + lr;
-                    const int c = (2 * s2 + lh) ^ ((r >> 1) & 3);
-                    bp[j] = *reinterpret_cast<const uint4*>(cur + A_ST + r * 64 + c * 16);
-                }
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const int ks = 2 * s2 + t;
-                    v4i a[2], bb[2];
-#pragma unroll
-                    for (int ii = 0; ii < 2; ii++) {
-                        const int r = 64 * wm + 32 * ii + lr;
-                        const int c = (4 * s2 + 2 * lh + t) ^ (r & 7);
-                        a[ii] = *reinterpret_cast<const v4i*>(cur + r * 128 + c * 16);
-                    }
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        const uint32_t x0 = t ? bp[j].z : bp[j].x, x1 = t ? bp[j].w : bp[j].y;
-                        bb[j] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
-                    }
-#pragma unroll
-                    for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                        for (int j = 0; j < 2; j++)
-                            acc[ii][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ii], bb[j],
-                                                                               ks == 0 ? zero16 : acc[ii][j], 0, 0, 0);
-                }
+                const int r = 64 * wn + 32 * j + lr;
+                const int c = (2 * s2 + lh) ^ ((r >> 2) & 3);
+                dst[j][s2] = *reinterpret_cast<const uint4*>(stg + A_ST + r * 64 + c * 16);
             }
+    };
+    const v16i zero16 = {};
+    auto mma = [&](v16i& acc, const v4i (&a)[4], const v4i (&bb)[4]) {
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], bb[0], zero16, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], bb[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[2], bb[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[3], bb[3], acc, 0, 0, 0);
+    };
+    // fold of tile (ii, j): lane holds column 32j + lr, rows 8q + 4lh + e
+    auto fold = [&](v16i& fa, const v16i& acc, const float* ls, int ii, int j, const Unit& x) {
+        const float sbv = ls[128 + 64 * wn + 32 * j + lr];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 v = *reinterpret_cast<const float4*>(ls + 64 * wm + 32 * ii + 8 * q + 4 * lh);
+            const float sv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int r = 4 * q + e;
+                fa[r] = __float_as_int(fmaf((float)acc[r], sv[e] * sbv, __int_as_float(fa[r])));
+            }
+        }
+        if (GSUM) {
+            const int nn = x.bn() + 64 * wn + 32 * j + lr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (m < M && nn < N) gsum[((size_t)m * N + nn) * NG + x.g] = acc[r] >> 4;
+            }
+        }
+    };
 
-            // --- fold: lane holds column 32j + lr, rows 8q + 4lh + e of tile (ii, j)
-            const float* ls = reinterpret_cast<const float*>(cur + A_ST + B_ST);
-            float sbv[2];
+    // prologue: DMA of units 0..3 (clamped to the last unit), then fragments of unit 0
+    Unit cu = unit_of((int)u0, NG, ntm);
+    Unit iu = cu;
+    DmaOff off = dma_offsets(iu, M, N, K, w, lane);
+    auto advance = [&]() {
+        iu.next(NG, ntm);
+        if (iu.g == 0) off = dma_offsets(iu, M, N, K, w, lane);
+    };
 #pragma unroll
-            for (int j = 0; j < 2; j++) sbv[j] = ls[128 + 64 * wn + 32 * j + lr];
+    for (int s = 0; s < 4; s++) {
+        if (s > 0 && s < n) advance();
+        issue(stage(s), slot(s), A, W, sa, sb, M, N, K, iu, off, w);
+    }
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * DMA_PER_UNIT) : "memory");
+    __syncthreads();
+    v4i a0[4], a1[4];
+    uint4 bp[2][2];
+    read_a(a0, stage(0), 0);
+    read_b(bp, stage(0));
+
+    bool flushed = false;
+    for (int i = 0; i < n; i++) {
+        const Unit x = cu;
+        cu.next(NG, ntm);
+        const float* ls = reinterpret_cast<const float*>(slot(i));
+        v4i bu[2][4];
 #pragma unroll
-            for (int ii = 0; ii < 2; ii++) {
+        for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 v = *reinterpret_cast<const float4*>(ls + 64 * wm + 32 * ii + 8 * q + 4 * lh);
-                    const float sv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int r = 4 * q + e;
-                            const float f = __int_as_float(facc[ii][j][r]);
-                            facc[ii][j][r] = __float_as_int(fmaf((float)acc[ii][j][r], sv[e] * sbv[j], f));
-                        }
-                }
+            for (int ks = 0; ks < 4; ks++) {
+                const uint4 p = bp[j][ks >> 1];
+                const uint32_t x0 = (ks & 1) ? p.z : p.x, x1 = (ks & 1) ? p.w : p.y;
+                bu[j][ks] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
             }
-            if (GSUM) {
+        read_a(a1, stage(i), 1);
+        v16i accA, accB;
+        mma(accA, a0, bu[0]);                       // tile (0,0)
+        mma(accB, a0, bu[1]);                       // tile (0,1)
+        fold(facc[0][0], accA, ls, 0, 0, x);
+        // the DMA of unit i+1 has landed once at most the 2 younger units' loads are pending;
+        // every wave has finished reading stage i (its LDS reads retire before the barrier)
+        // C stores of a tile flushed at the end of the previous unit are younger than the
+        // DMA awaited here; vmcnt retires in order, so a bound of 63 still covers that DMA
+        if (flushed) asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
+        flushed = false;
+        __syncthreads();
+        if (i + 4 < n) advance();
+        issue(stage(i), slot(i + 4), A, W, sa, sb, M, N, K, iu, off, w);
+        read_a(a0, stage(i + 1), 0);
+        read_b(bp, stage(i + 1));
+        mma(accA, a1, bu[0]);                       // tile (1,0)
+        fold(facc[0][1], accB, ls, 0, 1, x);
+        mma(accB, a1, bu[1]);                       // tile (1,1)
+        fold(facc[1][0], accA, ls, 1, 0, x);
+        fold(facc[1][1], accB, ls, 1, 1, x);
+
+        // --- end of this workgroup's segment of tile x.t: publish it
+        if (x.g == NG - 1 || i == n - 1) {
+            flushed = true;
+            const long long tb = (long long)x.t * NG, te = tb + NG;
+            bool write_c = true;
+            if (!(u0 <= tb && u1 >= te)) {
+                const int slt = (x.t == first_tile) ? 0 : 1;
+                float* my = part + ((size_t)b * 2 + slt) * PART_FLOATS + (size_t)threadIdx.x * 4;
+                v4f pv[16];
 #pragma unroll
                 for (int ii = 0; ii < 2; ii++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        const int nn = x.bn() + 64 * wn + 32 * j + lr;
+                    for (int j = 0; j < 2; j++)
 #pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
-                            if (m < M && nn < N) gsum[((size_t)m * N + nn) * NG + x.g] = acc[ii][j][r] >> 4;
-                        }
-                    }
-            }
-
-            // --- end of this workgroup's segment of tile x.t: publish it
-            if (x.g == NG - 1 || i == n - 1) {
-                const long long tb = (long long)x.t * NG, te = tb + NG;
-                bool write_c = true;
-                if (!(u0 <= tb && u1 >= te)) {
-                    // split tile: partial -> workspace slot, last contributor combines
-                    const int slot = (x.t == first_tile) ? 0 : 1;
-                    // layout [slot][k/4][thread][4]: each store instruction writes 8 KB contiguous
-                    float* my = part + ((size_t)b * 2 + slot) * PART_FLOATS + (size_t)threadIdx.x * 4;
-                    v4f pv[16];
+                        for (int r4 = 0; r4 < 4; r4++)
+                            pv[(ii * 2 + j) * 4 + r4] = v4f{
+                                __int_as_float(facc[ii][j][4 * r4]), __int_as_float(facc[ii][j][4 * r4 + 1]),
+                                __int_as_float(facc[ii][j][4 * r4 + 2]), __int_as_float(facc[ii][j][4 * r4 + 3])};
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                store8_dev16(my, pv);
+                store8_dev16(my + (size_t)8 * NT * 4, pv + 8);
+                __syncthreads();
+                const int wf = owner_of(tb, T, P), wl = owner_of(te - 1, T, P);
+                if (threadIdx.x == 0)
+                    s_flag = __hip_atomic_fetch_add(cnt + x.t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                             wl - wf;
+                __syncthreads();
+                write_c = s_flag;
+                if (write_c) {
 #pragma unroll
                     for (int ii = 0; ii < 2; ii++)
 #pragma unroll
                         for (int j = 0; j < 2; j++)
 #pragma unroll
-                            for (int r4 = 0; r4 < 4; r4++)
-                                pv[(ii * 2 + j) * 4 + r4] = v4f{
-                                    __int_as_float(facc[ii][j][4 * r4]), __int_as_float(facc[ii][j][4 * r4 + 1]),
-                                    __int_as_float(facc[ii][j][4 * r4 + 2]), __int_as_float(facc[ii][j][4 * r4 + 3])};
-                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // DMA still in flight counts too
-                    store8_dev16(my, pv);
-                    store8_dev16(my + (size_t)8 * NT * 4, pv + 8);
-                    __syncthreads();
-                    const int wf = owner_of(tb, T, P), wl = owner_of(te - 1, T, P);
-                    if (threadIdx.x == 0)
-                        s_flag = __hip_atomic_fetch_add(cnt + x.t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                                 wl - wf;
-                    __syncthreads();
-                    write_c = s_flag;
-                    if (write_c) {
-                        // sum the contributors' partials in workgroup order (deterministic)
+                            for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
+                    for (int v = wf; v <= wl; v++) {
+                        const int ft = (int)((T * v / P) / NG);
+                        const float* pp = part + ((size_t)v * 2 + (ft == x.t ? 0 : 1)) * PART_FLOATS +
+                                          (size_t)threadIdx.x * 4;
+                        v4f pv2[16];
+                        load8_dev16(pv2, pp);
+                        load8_dev16(pv2 + 8, pp + (size_t)8 * NT * 4);
 #pragma unroll
                         for (int ii = 0; ii < 2; ii++)
 #pragma unroll
                             for (int j = 0; j < 2; j++)
 #pragma unroll
-                                for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
-                        for (int v = wf; v <= wl; v++) {
-                            const int ft = (int)((T * v / P) / NG);
-                            const float* pp = part + ((size_t)v * 2 + (ft == x.t ? 0 : 1)) * PART_FLOATS +
-                                              (size_t)threadIdx.x * 4;
-                            v4f pv[16];
-                            load8_dev16(pv, pp);
-                            load8_dev16(pv + 8, pp + (size_t)8 * NT * 4);
-#pragma unroll
-                            for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                                for (int j = 0; j < 2; j++)
-#pragma unroll
-                                    for (int r = 0; r < 16; r++) {
-                                        const float f = __int_as_float(facc[ii][j][r]);
-                                        facc[ii][j][r] = __float_as_int(f + pv[(ii * 2 + j) * 4 + (r >> 2)][r & 3]);
-                                    }
-                        }
-                        if (threadIdx.x == 0)
-                            __hip_atomic_store(cnt + x.t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-                if (write_c) {
-#pragma unroll
-                    for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                        for (int j = 0; j < 2; j++) {
-                            const int nn = x.bn() + 64 * wn + 32 * j + lr;
-                            if (nn < N)
-#pragma unroll
                                 for (int r = 0; r < 16; r++) {
-                                    const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
-                                    if (m < M) C[(size_t)m * N + nn] = __int_as_float(facc[ii][j][r]) * 0.0625f;
+                                    const float f = __int_as_float(facc[ii][j][r]);
+                                    facc[ii][j][r] = __float_as_int(f + pv2[(ii * 2 + j) * 4 + (r >> 2)][r & 3]);
                                 }
-                        }
+                    }
+                    if (threadIdx.x == 0)
+                        __hip_atomic_store(cnt + x.t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+            }
+            if (write_c) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ii++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < 2; j++) {
+                        const int nn = x.bn() + 64 * wn + 32 * j + lr;
+                        if (nn < N)
 #pragma unroll
-                        for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
+                            for (int r = 0; r < 16; r++) {
+                                const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
+                                if (m < M) C[(size_t)m * N + nn] = __int_as_float(facc[ii][j][r]) * 0.0625f;
+                            }
+                    }
             }
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the clamped tail DMA before exit
 }
-
 }  // namespace
 
 GemmPlan gemm_plan(int M, int N, int K, int cus) {
