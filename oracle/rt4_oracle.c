@@ -187,6 +187,67 @@ void rt4o_quant_rows_a4(const float* x, int rows, int K, int G, int in_stride, i
         }
 }
 
+/* ------------------------------------------------------ weight quantizer -- */
+
+/* float -> binary16 bit pattern with the reference converter's own rounding
+ * (tools/convert.c:102-120).  Normal results add 0x1000 plus the kept lsb to the
+ * 23-bit mantissa before truncating 13 bits, so exact ties round away from zero
+ * (and one pattern just below a tie with an odd kept lsb rounds up too); this is
+ * not numpy's round-to-nearest-even, and the scales must match it bit for bit. */
+uint16_t rt4o_f32_to_f16_conv(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint32_t s = (u >> 16) & 0x8000u;
+    int32_t e = (int32_t)((u >> 23) & 0xFFu) - 127 + 15;
+    uint32_t m = u & 0x7FFFFFu;
+    if (((u >> 23) & 0xFFu) == 0xFFu) return (uint16_t)(s | 0x7C00u | (m ? 0x200u : 0u));
+    if (e >= 0x1F) return (uint16_t)(s | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)s;
+        m |= 0x800000u;
+        const int sh = 14 - e;
+        const uint32_t half = 1u << (sh - 1);
+        return (uint16_t)(s | ((m + half - 1 + ((m >> sh) & 1u)) >> sh));
+    }
+    uint32_t r = m + 0x1000u + ((m >> 13) & 1u);
+    if (r & 0x800000u) {
+        r = 0;
+        if (++e >= 0x1F) return (uint16_t)(s | 0x7C00u);
+    }
+    return (uint16_t)(s | ((uint32_t)e << 10) | (r >> 13));
+}
+
+/* The converter's int4 weight quantizer (tools/convert.c:338-360, bits = 4):
+ * per (row, 128-group) s = amax>0 ? amax/7 : 1, stored as f16 with the rounding
+ * above; q = clamp(roundf(w * (1/s)), -7, 7) with the fp32 s (not the rounded
+ * f16), packed two's complement, low nibble = even k (docs/FORMAT.md:61-73).
+ * w f32 [N][K] -> wq u32 [N][K/8], ws u16 [N][K/128]. */
+void rt4o_quant_weight_rows(const float* w, int N, int K, uint32_t* wq, uint16_t* ws) {
+    const int NG = K / RT4O_GROUP;
+    for (int n = 0; n < N; n++)
+        for (int g = 0; g < NG; g++) {
+            const float* blk = w + (size_t)n * K + (size_t)g * RT4O_GROUP;
+            float amax = 0.f;
+            for (int i = 0; i < RT4O_GROUP; i++) {
+                const float a = fabsf(blk[i]);
+                if (a > amax) amax = a;
+            }
+            const float s = amax > 0.f ? amax / 7.0f : 1.0f;
+            ws[(size_t)n * NG + g] = rt4o_f32_to_f16_conv(s);
+            const float inv = 1.0f / s;
+            for (int d = 0; d < RT4O_GROUP / 8; d++) {
+                uint32_t word = 0;
+                for (int e = 0; e < 8; e++) {
+                    float q = roundf(blk[8 * d + e] * inv);
+                    if (q > 7.f) q = 7.f;
+                    if (q < -7.f) q = -7.f;
+                    word |= ((uint32_t)(int)q & 0xFu) << (4 * e);
+                }
+                wq[(size_t)n * (K / 8) + (size_t)g * (RT4O_GROUP / 8) + d] = word;
+            }
+        }
+}
+
 /* RT4 row-major fp16 scales -> fp32 group-major, src/model.cpp:190-202. */
 void rt4o_make_group_major(const uint16_t* ws, int N, int NG, float* out) {
     for (int n = 0; n < N; n++)

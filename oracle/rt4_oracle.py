@@ -37,6 +37,8 @@ def lib() -> ctypes.CDLL:
             "rt4o_quant_rows_i8": ([P, I, I, I, I, I, P, P], None),
             "rt4o_quant_rows_a4": ([P, I, I, I, I, I, P, P], None),
             "rt4o_make_group_major": ([P, I, I, P], None),
+            "rt4o_f32_to_f16_conv": ([ctypes.c_float], ctypes.c_uint16),
+            "rt4o_quant_weight_rows": ([P, I, I, P, P], None),
             "rt4o_gemv_groupsums": ([P, P, I, I, I, P], None),
             "rt4o_gemv_fold": ([P, P, P, I, I, I, P], None),
             "rt4o_gemv_w4a8": ([P, P, P, I, I, I, P], None),
@@ -112,6 +114,22 @@ def quant_rows_a4(x: np.ndarray, rows: int, K: int, G: int = GROUP, in_stride: i
     sc = np.empty((K // G, rows), np.float32)
     lib().rt4o_quant_rows_a4(_p(x), rows, K, G, in_stride, in_off, _p(q), _p(sc))
     return q, sc
+
+
+def f32_to_f16_conv(x: float) -> int:
+    """The reference converter's float -> f16 bits (tools/convert.c:102-120)."""
+    return int(lib().rt4o_f32_to_f16_conv(float(x)))
+
+
+def quant_weight_rows(w: np.ndarray):
+    """The reference converter's int4 weight quantizer (tools/convert.c:338-360):
+    w f32 [N, K] -> (wq uint32 [N, K/8], ws uint16 [N, K/128])."""
+    w = _c(w, np.float32)
+    N, K = w.shape
+    wq = np.empty((N, K // 8), np.uint32)
+    ws = np.empty((N, K // GROUP), np.uint16)
+    lib().rt4o_quant_weight_rows(_p(w), N, K, _p(wq), _p(ws))
+    return wq, ws
 
 
 def make_group_major(ws: np.ndarray) -> np.ndarray:
