@@ -36,6 +36,22 @@ void k_quant_rows_a8(u32* qh, u32* ql, float* sc, float* sc16, const float* x, i
 void k_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int in_stride = 0,
                   int in_off = 0);
 
+// src/kernels.h:40 -- Q quantizer of all heads for the attention kernel.
+void k_attn_q_quant(u32* qq, float* qs, const float* x, int T, int H, int D, int G, int TP);
+
+// src/kernels.h:50,53 -- KV cache appends (K per (key, 128-dim group); V per (64-key tile, dim)).
+void k_kv_append_k(u32* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                   int kv_total);
+void k_kv_append_v(u32* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D,
+                   int BG, int kv_total);
+
+// src/kernels.h:81 -- int4-KV causal attention.  The prefill kernel serves both
+// of the reference's branches (see shim.cpp); pout/pmax/psum/max_split are unused.
+void k_attention(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc,
+                 const u32* vc, const float* vsc, int n_q, int n_row, int n_kv, int off, int n_tile,
+                 int n_heads, int ratio, int kv_cap, float* pout, float* pmax, float* psum,
+                 int max_split);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -133,6 +133,41 @@ int rt4_gemm_w4a8_groupsums(int32_t* gsum, float* c, const uint32_t* wq, const f
  * make_group_major (src/model.cpp:190-202), on the device. */
 int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream);
 
+/* ------------------------------------------------ int4-KV attention ------ */
+/* Head dim 256; Q and K quantized per (row, 128-dim group), V per (64-key tile,
+ * dim), all s = amax/7 with codes clamp(lrintf(x/s), -8, 7).  Layouts:
+ *   qq u32 [H][TP][D/8], qsc f32 [H][D/G][TP]
+ *   kc u32 [KVH][cap][D/8], ksc f32 [KVH][D/G][cap]
+ *   vc u32 [KVH][cap/8][D] (8 consecutive keys per dword, low nibble = even key),
+ *   vsc f32 [KVH][cap/BG][D];  x, kf, vf f32 [T][H][D]. */
+
+/* Q quantizer of all heads.  Replaces k_attn_q_quant (src/kernels.h:40,
+ * src/k_new.hip:228-260), bit for bit; rows >= T are not written. */
+int rt4_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP,
+                     void* stream);
+
+/* K cache append at keys t0..t0+T-1.  Replaces k_kv_append_k (src/kernels.h:50,
+ * src/k_new.hip:327-350), bit for bit. */
+int rt4_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                    int kv_total, void* stream);
+
+/* V cache append through the f32 stage [H][BG][D] of the current partial tile:
+ * every touched tile is re-quantized from its valid slots.  Replaces
+ * k_kv_append_v (src/kernels.h:53, src/k_new.hip:351-399), bit for bit. */
+int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
+                    int D, int BG, int kv_total, void* stream);
+
+/* Causal int4 FlashAttention prefill, GQA (KV head = head / ratio), out f32
+ * [n_heads][n_q][256] = softmax(Q K^T) V with the reference's fixed-point
+ * algorithm: per 64-key tile P = clamp(int(7 exp(s - m_tile) + 0.5), 0, 7) and
+ * online rescaling.  Query row i has position off + i.  Replaces the prefill
+ * branch of k_attention (src/kernels.h:81, src/k_fa.hip:282-300; kernel fa_int4,
+ * kernels/flash_attn_core.h:74-435).  n_q % 64 == 0, kv_cap % 64 == 0,
+ * n_tile * 64 <= kv_cap; BG of the V cache must be 64. */
+int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
+                          const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv,
+                          int off, int n_tile, int n_heads, int ratio, int kv_cap, void* stream);
+
 /* ------------------------------------------- W4A4 siblings (link only) ---- */
 
 /* int4 activation quantizer.  Replaces k_quant_rows (src/kernels.h:36,

@@ -1,0 +1,408 @@
+// attn.hip -- int4-KV causal FlashAttention prefill and its feeders, gfx950.
+//
+// Formats (the reference's KV cache, kernels/flash_attn_core.h:74-112 and
+// src/k_new.hip:228-399; head dim D = 256, quantization group 128 along D):
+//   qq  u32 [H][TP][32]      Q int4 codes, 8 dims per dword, low nibble = even dim
+//   qsc f32 [H][2][TP]       Q scale per (row, 128-dim group), s = amax/7
+//   kc  u32 [KVH][cap][32]   K codes, same packing;  ksc f32 [KVH][2][cap]
+//   vc  u32 [KVH][cap/8][256] V codes transposed: dword = 8 consecutive keys of
+//                             one dim, low nibble = even key
+//   vsc f32 [KVH][cap/64][256] V scale per (64-key tile, dim)
+//   out f32 [H][TP][256]
+//
+// Prefill kernel (restates fa_int4, kernels/flash_attn_core.h:74-435).  Per
+// 64-key tile and query row: S = Σ_g I_g·sq_g·sk_g over the two 128-dim groups
+// (I_g exact int32 dot products of the codes), causal mask, tile row max mt,
+// P = clamp(int(7·2^((S-mt)·log2e) + 0.5), 0, 7), online rescale alpha =
+// 2^((r_old-r_new)·log2e), beta = 2^((mt-r_new)·log2e), L = L·alpha + Σp·beta/7,
+// O = O·alpha + (Σ_k P·Vcode)·(beta/7)·vsc; out = O / L.
+//
+// MI355X design.  A workgroup is 64 query rows of one head, 4 waves of 16 rows.
+// Both contractions run on v_mfma_i32_16x16x64_i8 in transposed form so that a
+// lane always owns one query row:
+//   S^T[key][q] = K·Q^T   A = K codes (x16 unpack), B = the wave's Q codes
+//                         (resident, sign-extended int8); a lane holds query
+//                         q = lane%16 and keys 16t + 4G + r (G = lane/16,
+//                         r = 0..3) of the four 16-key subtiles t.
+//   O^T[d][q]  = V^T·P^T  B = P straight from those registers (4 dwords: the
+//                         lane's 16 keys), A = V codes laid out in LDS with the
+//                         same key order, so P never leaves the registers.
+// Row max and row sum over a query's 64 keys are 15 in-lane ops plus two
+// cross-lane steps (xor 16, xor 32).  The workgroup unpacks each K/V tile once
+// into LDS in MFMA operand order (K: x16 bytes per (subtile, k-step, lane);
+// V: v_perm of the x16 bytes into [r0 r2 r1 r3] per 4 keys), so the waves only
+// issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
+// position are skipped: the reference processes them but every entry is masked,
+// which leaves its state bit-for-bit unchanged.
+#include "rt4_dev.h"
+#include "rt4_internal.h"
+
+namespace rt4 {
+
+namespace {
+
+constexpr int HD = 256;           // head dim
+constexpr int KDW = HD / 8;       // dwords per K / Q row
+constexpr int BNK = 64;           // keys per tile
+constexpr int QROWS = 64;         // query rows per workgroup
+constexpr int NTA = 256;          // 4 waves
+constexpr float L2E = 1.4426950408889634f;
+
+__device__ __forceinline__ int sext4(uint32_t w, int e) { return ((int)(w << (28 - 4 * e))) >> 28; }
+
+// Sign-extended int8 codes of one dword in the interleaved order [c0 c2 c4 c6 | c1 c3 c5 c7].
+__device__ __forceinline__ uint2 codes_i8(uint32_t w) {
+    uint2 r;
+    r.x = (uint32_t)(sext4(w, 0) & 0xFF) | (uint32_t)(sext4(w, 2) & 0xFF) << 8 |
+          (uint32_t)(sext4(w, 4) & 0xFF) << 16 | (uint32_t)(sext4(w, 6) & 0xFF) << 24;
+    r.y = (uint32_t)(sext4(w, 1) & 0xFF) | (uint32_t)(sext4(w, 3) & 0xFF) << 8 |
+          (uint32_t)(sext4(w, 5) & 0xFF) << 16 | (uint32_t)(sext4(w, 7) & 0xFF) << 24;
+    return r;
+}
+
+// int4 code of x / s (s = amax/7 or 1), same IEEE ops as the reference quantizers.
+__device__ __forceinline__ uint32_t code4(float x, float s) {
+    return (uint32_t)clampi((int)lrintf(x / s), -8, 7) & 0xFu;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ feeders --
+
+// Q of all heads (restates attn_q_quant_k, src/k_new.hip:228-253): x f32 [T][H][D]
+// -> qq [H][TP][D/8], qs [H][D/G][TP].  One lane per 8 elements; a G-group is GL =
+// G/8 consecutive lanes.  Rows >= T are not written.
+template <int GL>
+__global__ __launch_bounds__(256) void attn_q_quant_k(uint32_t* __restrict__ qq, float* __restrict__ qs,
+                                                      const float* __restrict__ x, int T, int H, int D, int TP) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int dw = D >> 3;
+    if (i >= (size_t)T * H * dw) return;          // whole groups exit together
+    const int e8 = (int)(i % dw);
+    const int rh = (int)(i / dw), h = rh % H, r = rh / H;
+    const float* xr = x + (size_t)rh * D + 8 * e8;  // (r*H + h)*D
+    float v[8], amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        v[e] = xr[e];
+        amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = run_max<GL>(amax);
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
+    qq[((size_t)h * TP + r) * dw + e8] = w;
+    const int ng = D / (8 * GL);
+    if (e8 % GL == 0) qs[((size_t)h * ng + e8 / GL) * TP + r] = s;
+}
+
+// K cache append (restates kv_append_k_k, src/k_new.hip:327-347): kf f32 [T][H][D]
+// -> kc [H][kv_total][D/8], ksc [H][D/G][kv_total] at keys t0..t0+T-1.
+template <int GL>
+__global__ __launch_bounds__(256) void kv_append_k_k(uint32_t* __restrict__ kc, float* __restrict__ ksc,
+                                                     const float* __restrict__ kf, int t0, int T, int H, int D,
+                                                     int kv_total) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int dw = D >> 3;
+    if (i >= (size_t)T * H * dw) return;
+    const int e8 = (int)(i % dw);
+    const int th = (int)(i / dw), h = th % H, t = th / H;
+    const int kv = t0 + t;
+    const float* xr = kf + (size_t)th * D + 8 * e8;
+    float v[8], amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        v[e] = xr[e];
+        amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = run_max<GL>(amax);
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
+    kc[((size_t)h * kv_total + kv) * dw + e8] = w;
+    const int ng = D / (8 * GL);
+    if (e8 % GL == 0) ksc[((size_t)h * ng + e8 / GL) * kv_total + kv] = s;
+}
+
+// V cache append (restates kv_append_v_k, src/k_new.hip:351-392).  One thread per
+// (head, dim) walks the tiles the append touches: new values go into the fp32
+// stage [H][BG][D] (the current partial tile), the tile is re-quantized from its
+// valid slots, slots past the last valid one get code 0.  grid (H, D/64), 64 threads.
+__global__ __launch_bounds__(64) void kv_append_v_k(uint32_t* __restrict__ vc, float* __restrict__ vsc,
+                                                    float* __restrict__ stage, const float* __restrict__ vf,
+                                                    int t0, int T, int H, int D, int BG, int kv_total) {
+    const int h = blockIdx.x, d = blockIdx.y * 64 + threadIdx.x;
+    if (d >= D) return;
+    float* st = stage + (size_t)h * BG * D + d;
+    uint32_t* out = vc + (size_t)h * (kv_total / 8) * D;
+    int done = 0;
+    while (done < T) {
+        const int kv = t0 + done, tile = kv / BG, slot0 = kv % BG;
+        const int n = (T - done < BG - slot0) ? (T - done) : (BG - slot0);
+        for (int i = 0; i < n; i++) st[(size_t)(slot0 + i) * D] = vf[((size_t)(done + i) * H + h) * D + d];
+        const int nval = slot0 + n;
+        float amax = 0.f;
+        for (int i = 0; i < nval; i++) amax = fmaxf(amax, fabsf(st[(size_t)i * D]));
+        const float s = amax > 0.f ? amax / 7.f : 1.f;
+        vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
+        for (int i = 0; i < BG; i += 8) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = (i + e < nval) ? st[(size_t)(i + e) * D] : 0.f;
+                w |= code4(v, s) << (4 * e);
+            }
+            out[((size_t)tile * (BG / 8) + i / 8) * D + d] = w;
+        }
+        done += n;
+    }
+}
+
+// ---------------------------------------------------------------- prefill --
+
+__global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__ qq,
+                                                    const float* __restrict__ qsc,
+                                                    const uint32_t* __restrict__ kc,
+                                                    const float* __restrict__ ksc,
+                                                    const uint32_t* __restrict__ vc,
+                                                    const float* __restrict__ vsc, float* __restrict__ out,
+                                                    int n_q, int n_kv, int off, int n_tile, int ratio,
+                                                    int kv_cap) {
+    __shared__ __align__(16) unsigned char ku[4 * 4 * 64 * 16];   // [subtile][k-step][lane] x 16 B
+    __shared__ __align__(16) unsigned char vu[16 * 64 * 16];      // [dim tile][lane] x 16 B
+    __shared__ __align__(16) float ks_l[2 * BNK];
+    __shared__ __align__(16) float vs_l[HD];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
+    const int qi = lane & 15, G = lane >> 4;
+    const int head = blockIdx.y, vh = head / ratio;
+    const int q0 = blockIdx.x * QROWS;
+    const int qrow = q0 + 16 * w + qi;
+    qq += (size_t)head * n_q * KDW;
+    qsc += (size_t)head * 2 * n_q;
+    kc += (size_t)vh * kv_cap * KDW;
+    ksc += (size_t)vh * 2 * kv_cap;
+    vc += (size_t)vh * (kv_cap / 8) * HD;
+    vsc += (size_t)vh * (kv_cap / BNK) * HD;
+    out += (size_t)head * n_q * HD;
+
+    // tiles holding keys at or before this workgroup's last query position
+    int nt = (off + q0 + QROWS - 1) / BNK + 1;
+    nt = nt < n_tile ? nt : n_tile;
+
+    // resident Q operand: k-step s covers dims 64s + 16G .. +15 (dwords 8s+2G, 8s+2G+1)
+    v4i qop[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const uint2 wd = *reinterpret_cast<const uint2*>(qq + (size_t)qrow * KDW + 8 * s + 2 * G);
+        const uint2 a = codes_i8(wd.x), b = codes_i8(wd.y);
+        qop[s] = v4i{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
+    }
+    // S in log2 units: fold log2(e) and the 1/16 of the x16 K operand into the Q scales
+    const float A0 = qsc[qrow] * (L2E * 0.0625f), A1 = qsc[n_q + qrow] * (L2E * 0.0625f);
+
+    float O[16][4];
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) O[dt][r] = 0.f;
+    float rref = -1e30f, L = 0.f;
+
+    // staging registers: K rows (key tid%64, k-step tid/64: 8 dwords), V (dim tid: 8 key groups)
+    uint4 kr0, kr1;
+    uint32_t vr[8];
+    float ksr = 1.f, vsr = 1.f;
+    auto load_tile = [&](int t) {
+        const int kb = t * BNK;
+        const int kk = tid & 63, p = tid >> 6;
+        if (kb + kk < n_kv) {
+            const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)(kb + kk) * KDW + 8 * p);
+            kr0 = src[0];
+            kr1 = src[1];
+        } else {
+            kr0 = make_uint4(0, 0, 0, 0);
+            kr1 = kr0;
+        }
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const int k8 = kb / 8 + g;   // a group of 8 keys is read only if it is whole (flash_attn_core.h:150)
+            vr[g] = ((size_t)k8 * 8 + 8 <= (size_t)n_kv) ? vc[(size_t)k8 * HD + tid] : 0u;
+        }
+        if (tid < 2 * BNK) {
+            const int g = tid / BNK, j = kb + (tid % BNK);
+            ksr = j < kv_cap ? ksc[(size_t)g * kv_cap + j] : 1.f;
+        }
+        vsr = (t < kv_cap / BNK) ? vsc[(size_t)t * HD + tid] : 1.f;
+    };
+    auto store_tile = [&]() {
+        {   // K: x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16
+            const int kk = tid & 63, p = tid >> 6;
+            const uint32_t d[8] = {kr0.x, kr0.y, kr0.z, kr0.w, kr1.x, kr1.y, kr1.z, kr1.w};
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
+                                           odd_x16(d[2 * g + 1]));
+                *reinterpret_cast<uint4*>(ku + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
+            }
+        }
+        {   // V: lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3
+            uint32_t e[8], o[8];
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                e[g] = even_x16(vr[g]);
+                o[g] = odd_x16(vr[g]);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint32_t sel = (g & 1) ? 0x07060302u : 0x05040100u;
+                uint4 v;
+                v.x = __builtin_amdgcn_perm(o[0 + (g >> 1)], e[0 + (g >> 1)], sel);
+                v.y = __builtin_amdgcn_perm(o[2 + (g >> 1)], e[2 + (g >> 1)], sel);
+                v.z = __builtin_amdgcn_perm(o[4 + (g >> 1)], e[4 + (g >> 1)], sel);
+                v.w = __builtin_amdgcn_perm(o[6 + (g >> 1)], e[6 + (g >> 1)], sel);
+                *reinterpret_cast<uint4*>(vu + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
+            }
+        }
+        if (tid < 2 * BNK) ks_l[tid] = ksr;
+        vs_l[tid] = vsr;
+    };
+
+    const v4i zero = {0, 0, 0, 0};
+    if (nt > 0) load_tile(0);
+    for (int t = 0; t < nt; t++) {
+        const int kb = t * BNK;
+        __syncthreads();                 // the previous tile's operands are no longer read
+        store_tile();
+        __syncthreads();
+        if (t + 1 < nt) load_tile(t + 1);
+
+        // ---- S^T = K Q^T for the 4 subtiles of 16 keys
+        float sv[4][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            const v4i* kp = reinterpret_cast<const v4i*>(ku) + (kt * 4) * 64 + lane;
+            v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[0], qop[0], zero, 0, 0, 0);
+            a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[64], qop[1], a0, 0, 0, 0);
+            v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
+            const float4 k0 = *reinterpret_cast<const float4*>(ks_l + 16 * kt + 4 * G);
+            const float4 k1 = *reinterpret_cast<const float4*>(ks_l + BNK + 16 * kt + 4 * G);
+            const float s0[4] = {k0.x, k0.y, k0.z, k0.w}, s1[4] = {k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                sv[kt][r] = fmaf((float)a1[r], s1[r] * A1, (float)a0[r] * (s0[r] * A0));
+        }
+        if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -1e30f;
+        }
+        // ---- tile row max over the 64 keys of this lane's query
+        float m = sv[0][0];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) m = fmaxf(m, sv[kt][r]);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (m < -1e29f) m = rref;        // fully masked row: alpha = 1, beta folds to nothing
+        // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand
+        int isum = 0;
+        uint32_t pk[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            int pq[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = exp2f(sv[kt][r] - m) * 7.f;
+                int q = (int)(p + 0.5f);
+                q = q > 7 ? 7 : (q < 0 ? 0 : q);
+                pq[r] = q;
+                isum += q;
+            }
+            pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[2] << 8 | (uint32_t)pq[1] << 16 | (uint32_t)pq[3] << 24;
+        }
+        isum += __shfl_xor(isum, 16);
+        isum += __shfl_xor(isum, 32);
+        const float r_new = fmaxf(rref, m);
+        const float alpha = exp2f(rref - r_new);
+        const float beta = exp2f(m - r_new);
+        const float pb = beta * (1.f / 7.f);
+        L = L * alpha + (float)isum * (beta / 7.f);
+        rref = r_new;
+        // ---- O^T = V^T P^T, folded per dim tile
+        const v4i pop = {(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        const float pb16 = pb * 0.0625f;          // V is x16 unpacked
+        const bool rescale = !__all(alpha == 1.f);
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const v4i va = *(reinterpret_cast<const v4i*>(vu) + dt * 64 + lane);
+            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pop, zero, 0, 0, 0);
+            const float4 s4 = *reinterpret_cast<const float4*>(vs_l + 16 * dt + 4 * G);
+            const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float o = rescale ? O[dt][r] * alpha : O[dt][r];
+                O[dt][r] = fmaf((float)acc[r], pb16 * sc[r], o);
+            }
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float* orow = out + (size_t)qrow * HD + 4 * G;
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+        *reinterpret_cast<float4*>(orow + 16 * dt) =
+            make_float4(O[dt][0] * inv, O[dt][1] * inv, O[dt][2] * inv, O[dt][3] * inv);
+}
+
+// -------------------------------------------------------------- launchers --
+
+hipError_t launch_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP,
+                               hipStream_t st) {
+    const size_t n = (size_t)T * H * (D / 8);
+    if (n == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (G / 8) {
+        case 8: hipLaunchKernelGGL(attn_q_quant_k<8>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
+        case 16: hipLaunchKernelGGL(attn_q_quant_k<16>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
+        case 32: hipLaunchKernelGGL(attn_q_quant_k<32>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                              int kv_total, hipStream_t st) {
+    const size_t n = (size_t)T * H * (D / 8);
+    if (n == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (G / 8) {
+        case 8: hipLaunchKernelGGL(kv_append_k_k<8>, grid, dim3(256), 0, st, kc, ksc, kf, t0, T, H, D, kv_total); break;
+        case 16: hipLaunchKernelGGL(kv_append_k_k<16>, grid, dim3(256), 0, st, kc, ksc, kf, t0, T, H, D, kv_total); break;
+        case 32: hipLaunchKernelGGL(kv_append_k_k<32>, grid, dim3(256), 0, st, kc, ksc, kf, t0, T, H, D, kv_total); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
+                              int D, int BG, int kv_total, hipStream_t st) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_append_v_k, dim3(H, (D + 63) / 64), dim3(64), 0, st, vc, vsc, stage, vf, t0, T, H, D, BG,
+                       kv_total);
+    return hipGetLastError();
+}
+
+hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
+                          const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
+                          int n_heads, int ratio, int kv_cap, hipStream_t st) {
+    hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc, out,
+                       n_q, n_kv, off, n_tile, ratio, kv_cap);
+    return hipGetLastError();
+}
+
+}  // namespace rt4

@@ -292,4 +292,53 @@ int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* 
                       "rt4_make_group_major launch");
 }
 
+// ------------------------------------------------------------- attention --
+
+int rt4_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP,
+                     void* stream) {
+    if (!qq || !qs || !x) return fail(RT4_E_ARG, "k_attn_q_quant: null pointer");
+    if (G != 64 && G != 128 && G != 256) return fail(RT4_E_ARG, "k_attn_q_quant: group G=%d unsupported", G);
+    if (T < 0 || H < 1 || D <= 0 || D % G || TP < T)
+        return fail(RT4_E_SHAPE, "k_attn_q_quant: T=%d H=%d D=%d G=%d TP=%d", T, H, D, G, TP);
+    if (!aligned(x, 4) || !aligned(qq, 4) || !aligned(qs, 4)) return fail(RT4_E_ARG, "k_attn_q_quant: misaligned");
+    return hip_status(rt4::launch_attn_q_quant(qq, qs, x, T, H, D, G, TP, as_stream(stream)), "k_attn_q_quant launch");
+}
+
+int rt4_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                    int kv_total, void* stream) {
+    if (!kc || !ksc || !kf) return fail(RT4_E_ARG, "k_kv_append_k: null pointer");
+    if (G != 64 && G != 128 && G != 256) return fail(RT4_E_ARG, "k_kv_append_k: group G=%d unsupported", G);
+    if (t0 < 0 || T < 0 || H < 1 || D <= 0 || D % G || (long long)t0 + T > kv_total)
+        return fail(RT4_E_SHAPE, "k_kv_append_k: t0=%d T=%d H=%d D=%d G=%d kv_total=%d", t0, T, H, D, G, kv_total);
+    return hip_status(rt4::launch_kv_append_k(kc, ksc, kf, t0, T, H, D, G, kv_total, as_stream(stream)),
+                      "k_kv_append_k launch");
+}
+
+int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D,
+                    int BG, int kv_total, void* stream) {
+    if (!vc || !vsc || !stage || !vf) return fail(RT4_E_ARG, "k_kv_append_v: null pointer");
+    if (t0 < 0 || T < 0 || H < 1 || D <= 0 || BG <= 0 || BG % 8 || kv_total % BG || (long long)t0 + T > kv_total)
+        return fail(RT4_E_SHAPE, "k_kv_append_v: t0=%d T=%d H=%d D=%d BG=%d kv_total=%d", t0, T, H, D, BG,
+                    kv_total);
+    return hip_status(rt4::launch_kv_append_v(vc, vsc, stage, vf, t0, T, H, D, BG, kv_total, as_stream(stream)),
+                      "k_kv_append_v launch");
+}
+
+int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
+                          const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
+                          int n_tile, int n_heads, int ratio, int kv_cap, void* stream) {
+    if (!out || !qq || !qsc || !kc || !ksc || !vc || !vsc) return fail(RT4_E_ARG, "k_attention: null pointer");
+    if (n_q < 64 || n_q % 64 || n_kv < 1 || n_kv > kv_cap || off < 0 || kv_cap % 64 || n_tile < 1 ||
+        (long long)n_tile * 64 > kv_cap || n_heads < 1 || ratio < 1 || n_heads % ratio || n_q > 65535 * 64)
+        return fail(RT4_E_SHAPE,
+                    "k_attention: n_q=%d (multiple of 64) n_kv=%d off=%d n_tile=%d n_heads=%d ratio=%d kv_cap=%d",
+                    n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap);
+    if (!aligned(qq, 16) || !aligned(kc, 16) || !aligned(vc, 4) || !aligned(out, 16) || !aligned(qsc, 4) ||
+        !aligned(ksc, 4) || !aligned(vsc, 4))
+        return fail(RT4_E_ARG, "k_attention: misaligned pointer (qq, kc, out need 16 bytes)");
+    return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
+                                          kv_cap, as_stream(stream)),
+                      "k_attention launch");
+}
+
 }  // extern "C"

@@ -51,4 +51,15 @@ hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint
                             float* part, int* cnt, hipStream_t st);
 hipError_t launch_zero_i32(int* p, size_t n, hipStream_t st);
 
+// ---- int4-KV attention (attn.hip); head dim 256, Q/K groups of 128, V tiles of 64 keys
+hipError_t launch_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP,
+                               hipStream_t st);
+hipError_t launch_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                              int kv_total, hipStream_t st);
+hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
+                              int D, int BG, int kv_total, hipStream_t st);
+hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
+                          const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
+                          int n_heads, int ratio, int kv_cap, hipStream_t st);
+
 }  // namespace rt4

@@ -41,3 +41,36 @@ void k_gemm_i4_a8(float* c, float* c2, const u32* wq, const float* wsc_gm, const
     if (rt4_gemm_w4a8(c, c2, wq, wsc_gm, ah, al, sc, sc16, M, N, K, nullptr) != RT4_OK)
         die("k_gemm_i4_a8");
 }
+
+// src/k_new.hip:254-260
+void k_attn_q_quant(u32* qq, float* qs, const float* x, int T, int H, int D, int G, int TP) {
+    if (rt4_attn_q_quant(qq, qs, x, T, H, D, G, TP, nullptr) != RT4_OK) die("k_attn_q_quant");
+}
+
+// src/k_new.hip:348-350
+void k_kv_append_k(u32* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G, int kv_total) {
+    if (rt4_kv_append_k(kc, ksc, kf, t0, T, H, D, G, kv_total, nullptr) != RT4_OK) die("k_kv_append_k");
+}
+
+// src/k_new.hip:393-399
+void k_kv_append_v(u32* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D, int BG,
+                   int kv_total) {
+    if (rt4_kv_append_v(vc, vsc, stage, vf, t0, T, H, D, BG, kv_total, nullptr) != RT4_OK) die("k_kv_append_v");
+}
+
+// src/k_fa.hip:282-300.  Both branches run the prefill kernel here: the
+// reference's single-row decode kernel (fa_decode_k, fp32 P with split-KV) is
+// not rebuilt, so a decode call (n_row == 1, off + 1 == n_kv) takes the path
+// the reference takes under RT_ATTN_OLD=1; the split-KV scratch is unused.
+void k_attention(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc, const u32* vc,
+                 const float* vsc, int n_q, int n_row, int n_kv, int off, int n_tile, int n_heads, int ratio,
+                 int kv_cap, float* pout, float* pmax, float* psum, int max_split) {
+    (void)n_row;
+    (void)pout;
+    (void)pmax;
+    (void)psum;
+    (void)max_split;
+    if (rt4_attention_prefill(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap,
+                              nullptr) != RT4_OK)
+        die("k_attention");
+}

@@ -10,6 +10,9 @@ Reference interface mirrored (src/kernels.h of K100LC-RT4):
     k_quant_rows_a8  -> quant_rows_a8        (src/kernels.h:43)
     k_gemm_i4_a8     -> gemm_w4a8            (src/kernels.h:32)
     k_quant_rows     -> quant_rows_a4        (src/kernels.h:36)
+    k_attn_q_quant   -> attn_q_quant         (src/kernels.h:40)
+    k_kv_append_k/v  -> kv_append_k / _v     (src/kernels.h:50, :53)
+    k_attention      -> attention_prefill    (src/kernels.h:81, prefill branch)
 plus the pieces those wrappers launch internally (quant_act_a8, gemv_w4a8_q).
 """
 from __future__ import annotations
@@ -29,6 +32,7 @@ C_EXPORTS = (
     "rt4_gemv_w4a8", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
     "rt4_make_group_major", "rt4_quant_rows_a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
+    "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
 )
 # The reference-compatible C++ entry points (include/rt4_kernels.h), mangled.
 CXX_EXPORTS = (
@@ -36,6 +40,10 @@ CXX_EXPORTS = (
     "_Z15k_quant_rows_a8PjS_PfS0_PKfiiiii",
     "_Z12k_quant_rowsPjPfPKfiiiii",
     "_Z12k_gemm_i4_a8PfS_PKjPKfS1_S1_S3_S3_iii",
+    "_Z14k_attn_q_quantPjPfPKfiiiii",
+    "_Z13k_kv_append_kPjPfPKfiiiiii",
+    "_Z13k_kv_append_vPjPfS0_PKfiiiiii",
+    "_Z11k_attentionPfPKjPKfS1_S3_S1_S3_iiiiiiiiS_S_S_i",
 )
 
 
@@ -60,6 +68,10 @@ _SIGS = {
     "rt4_gemm_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemm_w4a8_i8": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemm_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_attn_q_quant": [_P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "rt4_kv_append_k": [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_kv_append_v": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_attention_prefill": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
 }
 
 
@@ -259,3 +271,51 @@ def gemm_w4a8(wq, wsc_gm, qh, ql, sc, sc16, out=None, c2=None):
     _check(lib().rt4_gemm_w4a8(_ptr(c), _ptr(c2), _ptr(wq), _ptr(wsc_gm), _ptr(qh), _ptr(ql), _ptr(sc),
                                _ptr(sc16), M, N, K, _stream()))
     return c
+
+
+# ------------------------------------------------------------- attention ----
+HEAD_DIM = 256
+KV_TILE = 64
+
+
+def attn_q_quant(x, TP: int, G: int = GROUP, qq=None, qs=None):
+    """k_attn_q_quant: x f32 [T, H, D] -> (qq int32 [H, TP, D/8], qs f32 [H, D/G, TP]).
+    Rows >= T keep the buffers' contents (new buffers: zero codes, unit scales)."""
+    torch = _torch()
+    T, H, D = x.shape
+    if qq is None:
+        qq = torch.zeros((H, TP, D // 8), dtype=torch.int32, device=x.device)
+    if qs is None:
+        qs = torch.ones((H, D // G, TP), dtype=torch.float32, device=x.device)
+    _check(lib().rt4_attn_q_quant(_ptr(qq), _ptr(qs), _ptr(x), T, H, D, G, TP, _stream()))
+    return qq, qs
+
+
+def kv_append_k(kc, ksc, kf, t0: int, G: int = GROUP):
+    """k_kv_append_k, in place: kc int32 [H, kv_total, D/8], ksc f32 [H, D/G, kv_total]; kf f32 [T, H, D]."""
+    T, H, D = kf.shape
+    _check(lib().rt4_kv_append_k(_ptr(kc), _ptr(ksc), _ptr(kf), t0, T, H, D, G, kc.shape[1], _stream()))
+
+
+def kv_append_v(vc, vsc, stage, vf, t0: int):
+    """k_kv_append_v, in place: vc int32 [H, kv_total/8, D], vsc f32 [H, kv_total/BG, D],
+    stage f32 [H, BG, D]; vf f32 [T, H, D]."""
+    T, H, D = vf.shape
+    BG = stage.shape[1]
+    _check(lib().rt4_kv_append_v(_ptr(vc), _ptr(vsc), _ptr(stage), _ptr(vf), t0, T, H, D, BG,
+                                 vc.shape[1] * 8, _stream()))
+
+
+def attention_prefill(qq, qsc, kc, ksc, vc, vsc, n_kv: int, off: int, ratio: int,
+                      n_tile: int | None = None, out=None):
+    """Prefill branch of k_attention -> out f32 [H, n_q, 256]."""
+    torch = _torch()
+    H, n_q, _ = qq.shape
+    kv_cap = kc.shape[1]
+    if n_tile is None:
+        n_tile = (n_kv + KV_TILE - 1) // KV_TILE
+    if out is None:
+        out = torch.empty((H, n_q, HEAD_DIM), dtype=torch.float32, device=qq.device)
+    _check(lib().rt4_attention_prefill(_ptr(out), _ptr(qq), _ptr(qsc), _ptr(kc), _ptr(ksc), _ptr(vc), _ptr(vsc),
+                                       n_q, n_kv, off, n_tile, H, ratio, kv_cap, _stream()))
+    return out

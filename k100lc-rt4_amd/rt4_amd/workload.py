@@ -79,3 +79,26 @@ def acts_torch(M: int, K: int, outliers: bool = False, device="cuda", generator=
         mask = torch.rand((M, K), device=device, generator=generator) < 0.01
         x = torch.where(mask, x * 20.0, x)
     return x.contiguous()
+
+
+# ------------------------------------------------------------- attention --
+# 24 query heads, 4 KV heads (GQA 6:1), head dim 256, 1024 new query
+# rows over a 32768-token cache -> n_kv = 33792, query i at position 32768 + i.
+ATTN_C4 = {"H": 24, "KVH": 4, "D": 256, "n_q": 1024, "ctx": 32768}
+
+
+def attn_np(rng: np.random.Generator, T: int, n_kv: int, H: int, KVH: int, D: int = 256):
+    """fp16 N(0,1) Q [T, H, D] (scaled by 1/sqrt(D), as src/model.cpp:1067 does before
+    quantizing), K and V [n_kv, KVH, D], upcast to fp32."""
+    q = rng.standard_normal((T, H, D)).astype(np.float16).astype(np.float32) * np.float32(1.0 / np.sqrt(D))
+    k = rng.standard_normal((n_kv, KVH, D)).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((n_kv, KVH, D)).astype(np.float16).astype(np.float32)
+    return q.astype(np.float32), k, v
+
+
+def attn_torch(T: int, n_kv: int, H: int, KVH: int, D: int = 256, device="cuda", generator=None):
+    import torch
+    q = torch.randn((T, H, D), device=device, generator=generator).to(torch.float16).to(torch.float32) * (D ** -0.5)
+    k = torch.randn((n_kv, KVH, D), device=device, generator=generator).to(torch.float16).to(torch.float32)
+    v = torch.randn((n_kv, KVH, D), device=device, generator=generator).to(torch.float16).to(torch.float32)
+    return q.contiguous(), k.contiguous(), v.contiguous()

@@ -6,8 +6,9 @@
 // oracle (and of our HIP quantizers) on the same seeded inputs.  Nothing in the
 // product library links this.
 //
-// Only the quantizers are bound.  They are plain C++ float/integer code, so
-// their gfx950 build computes what the gfx926 build does.  The reference's
+// Only the quantizers (activation quantizers and the attention feeders) are
+// bound here.  They are plain C++ float/integer code, so their gfx950 build
+// computes what the gfx926 build does.  The reference's
 // GEMV/GEMM kernels are deliberately left out: their dot products are inline
 // assembly (v_dot4_i32_i8, kernels/gemv_w4a8_core.h:25-29; v_dot8_i32_i4,
 // kernels/gemm_core.h:167) written for gfx926, and a gfx950 build of
@@ -36,6 +37,19 @@ void ref_quant_rows_a8(u32* qh, u32* ql, float* sc, float* sc16, const float* x,
 void ref_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int in_stride,
                     int in_off) {
     k_quant_rows(q, sc, x, rows, K, G, in_stride, in_off);
+}
+
+// attention feeders (src/k_new.hip:228-399): Q quantizer and KV cache appends.
+void ref_attn_q_quant(u32* qq, float* qs, const float* x, int T, int H, int D, int G, int TP) {
+    k_attn_q_quant(qq, qs, x, T, H, D, G, TP);
+}
+void ref_kv_append_k(u32* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                     int kv_total) {
+    k_kv_append_k(kc, ksc, kf, t0, T, H, D, G, kv_total);
+}
+void ref_kv_append_v(u32* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D,
+                     int BG, int kv_total) {
+    k_kv_append_v(vc, vsc, stage, vf, t0, T, H, D, BG, kv_total);
 }
 
 void ref_sync(void) { hipDeviceSynchronize(); }

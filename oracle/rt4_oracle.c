@@ -27,6 +27,17 @@
  *                       (kernels/gemv_int4.hip:317-336), fp64 fold
  *   rt4o_gemm_*         per-group int = 16*I_h + I_l identity, fp64 fold as in
  *                       bench/int4_gemm2.cpp:104-123
+ *   rt4o_quant_weight_rows, rt4o_f32_to_f16_conv
+ *                       the reference converter (tools/convert.c) built in
+ *                       oracle/_ref, bit-identical output on a BF16 input
+ *   rt4o_attn_q_quant, rt4o_kv_append_k/v
+ *                       numpy restatement, split-append invariance of the V
+ *                       stage, and the reference's own feeder kernels built for
+ *                       gfx950 (GPU test)
+ *   rt4o_fa_rows        mode 0 against a numpy exact softmax over the dequantized
+ *                       cache; mode 1 against a numpy restatement of the tile
+ *                       algorithm and against mode 0 where the fixed-point scheme
+ *                       is exact (all scores equal)
  */
 #include <math.h>
 #include <stdint.h>
@@ -390,5 +401,188 @@ void rt4o_gemm_w4a4_points(const uint32_t* wq, const float* sb, const uint32_t* 
             if (Ig) Ig[(size_t)p * NG + g] = s;
         }
         if (c) c[p] = acc;
+    }
+}
+
+/* -------------------------------------------------- int4-KV attention -- */
+/* Head dim 256, Q/K quantized per (row, 128-dim group), V per (64-key tile, dim). */
+#define RT4O_HD 256
+#define RT4O_KD (RT4O_HD / 8)
+#define RT4O_QG 128
+#define RT4O_NQG (RT4O_HD / RT4O_QG)
+#define RT4O_BN 64
+
+/* int4 code of one element: s = amax>0 ? amax/7 : 1 applied by the caller. */
+static uint32_t rt4o_i4(float x, float s) {
+    int c = (int)lrintf(x / s);
+    c = c > 7 ? 7 : (c < -8 ? -8 : c);
+    return (uint32_t)c & 0xFu;
+}
+
+/* Q quantizer of all heads, restating attn_q_quant_k (src/k_new.hip:228-253):
+ * x f32 [T][H][D] -> qq u32 [H][TP][D/8], qs f32 [H][D/G][TP]; rows >= T untouched. */
+void rt4o_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP) {
+    const int ng = D / G;
+    for (int h = 0; h < H; h++)
+        for (int r = 0; r < T; r++)
+            for (int g = 0; g < ng; g++) {
+                const float* xr = x + ((size_t)r * H + h) * D + (size_t)g * G;
+                float amax = 0.f;
+                for (int j = 0; j < G; j++) amax = fmaxf(amax, fabsf(xr[j]));
+                const float s = amax > 0.f ? amax / 7.f : 1.f;
+                qs[((size_t)h * ng + g) * TP + r] = s;
+                uint32_t* qr = qq + ((size_t)h * TP + r) * (D / 8) + (size_t)(g * G) / 8;
+                for (int j = 0; j < G; j += 8) {
+                    uint32_t w = 0;
+                    for (int e = 0; e < 8; e++) w |= rt4o_i4(xr[j + e], s) << (4 * e);
+                    qr[j / 8] = w;
+                }
+            }
+}
+
+/* K cache append, restating kv_append_k_k (src/k_new.hip:327-347): kf f32 [T][H][D]
+ * -> kc u32 [H][kv_total][D/8], ksc f32 [H][D/G][kv_total] at keys t0..t0+T-1. */
+void rt4o_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, int H, int D, int G,
+                      int kv_total) {
+    const int ng = D / G;
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < H; h++)
+            for (int g = 0; g < ng; g++) {
+                const int kv = t0 + t;
+                const float* xr = kf + ((size_t)t * H + h) * D + (size_t)g * G;
+                float amax = 0.f;
+                for (int i = 0; i < G; i++) amax = fmaxf(amax, fabsf(xr[i]));
+                const float s = amax > 0.f ? amax / 7.f : 1.f;
+                ksc[((size_t)h * ng + g) * kv_total + kv] = s;
+                uint32_t* qr = kc + ((size_t)h * kv_total + kv) * (D / 8) + (size_t)(g * G) / 8;
+                for (int i = 0; i < G; i += 8) {
+                    uint32_t w = 0;
+                    for (int e = 0; e < 8; e++) w |= rt4o_i4(xr[i + e], s) << (4 * e);
+                    qr[i / 8] = w;
+                }
+            }
+}
+
+/* V cache append, restating kv_append_v_k (src/k_new.hip:351-392): the f32 stage
+ * [H][BG][D] holds the current partial tile; every tile the append touches is
+ * re-quantized from its valid slots (s = amax/7 per (tile, dim), slots beyond the
+ * last valid one are zero codes) into vc u32 [H][kv_total/8][D] (8 keys per dword,
+ * low nibble = even key) and vsc f32 [H][kv_total/BG][D]. */
+void rt4o_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
+                      int D, int BG, int kv_total) {
+    for (int h = 0; h < H; h++)
+        for (int d = 0; d < D; d++) {
+            float* st = stage + (size_t)h * BG * D + d;
+            uint32_t* out = vc + (size_t)h * (kv_total / 8) * D;
+            int done = 0;
+            while (done < T) {
+                const int kv = t0 + done, tile = kv / BG, slot0 = kv % BG;
+                const int n = (T - done < BG - slot0) ? (T - done) : (BG - slot0);
+                for (int i = 0; i < n; i++) st[(size_t)(slot0 + i) * D] = vf[((size_t)(done + i) * H + h) * D + d];
+                const int nval = slot0 + n;
+                float amax = 0.f;
+                for (int i = 0; i < nval; i++) amax = fmaxf(amax, fabsf(st[(size_t)i * D]));
+                const float s = amax > 0.f ? amax / 7.f : 1.f;
+                vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
+                for (int i = 0; i < BG; i += 8) {
+                    uint32_t w = 0;
+                    for (int e = 0; e < 8; e++) {
+                        const float v = (i + e < nval) ? st[(size_t)(i + e) * D] : 0.f;
+                        w |= rt4o_i4(v, s) << (4 * e);
+                    }
+                    out[((size_t)tile * (BG / 8) + i / 8) * D + d] = w;
+                }
+                done += n;
+            }
+        }
+}
+
+static int rt4o_nib(const uint32_t* row, int idx, int e) {
+    const int c = (int)((row[idx] >> (4 * e)) & 0xFu);
+    return c >= 8 ? c - 16 : c;
+}
+
+/* Dequantized operands of one q head / its kv head (values the kernel sees). */
+static double fa_q(const uint32_t* Q, const float* Qs, int n_q, int i, int d) {
+    return (double)rt4o_nib(Q + (size_t)i * RT4O_KD, d / 8, d % 8) * (double)Qs[(size_t)(d / RT4O_QG) * n_q + i];
+}
+static double fa_k(const uint32_t* K, const float* Ks, int kv_cap, int j, int d) {
+    return (double)rt4o_nib(K + (size_t)j * RT4O_KD, d / 8, d % 8) * (double)Ks[(size_t)(d / RT4O_QG) * kv_cap + j];
+}
+static double fa_v(const uint32_t* V, const float* Vs, int j, int d) {
+    return (double)rt4o_nib(V + (size_t)(j / 8) * RT4O_HD, d, j % 8) * (double)Vs[(size_t)(j / RT4O_BN) * RT4O_HD + d];
+}
+
+/* For query row i of q head `head`: its absolute position is off + i and it sees
+ * keys j <= min(off + i, n_kv - 1).  Layouts as fa_int4 reads them
+ * (kernels/flash_attn_core.h:74-112): qq [H][n_q][32], qsc [H][2][n_q],
+ * kc [KVH][kv_cap][32], ksc [KVH][2][kv_cap], vc [KVH][kv_cap/8][256],
+ * vsc [KVH][kv_cap/64][256], KV head = head / ratio.
+ *
+ * mode 0: exact softmax in fp64 over the same quantized Q/K/V, restating ref_rows
+ *         (kernels/flash_attn_int4.hip:146-170);
+ * mode 1: the kernel's fixed-point algorithm in fp64, restating ref_alg
+ *         (kernels/flash_attn_int4.hip:175-217): per 64-key tile the row max mt,
+ *         P = round(7 exp(s - mt)) in [0, 7], online rescale alpha = exp(r_old - r_new),
+ *         beta = exp(mt - r_new) / 7, out = O / L.
+ * out f64 [nrows][256]. */
+void rt4o_fa_rows(const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
+                  const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int kv_cap, int ratio,
+                  int head, const int32_t* rows, int nrows, int mode, double* out) {
+    const int vh = head / ratio;
+    const uint32_t* Q = qq + (size_t)head * n_q * RT4O_KD;
+    const float* Qs = qsc + (size_t)head * RT4O_NQG * n_q;
+    const uint32_t* K = kc + (size_t)vh * kv_cap * RT4O_KD;
+    const float* Ks = ksc + (size_t)vh * RT4O_NQG * kv_cap;
+    const uint32_t* V = vc + (size_t)vh * (kv_cap / 8) * RT4O_HD;
+    const float* Vs = vsc + (size_t)vh * (kv_cap / RT4O_BN) * RT4O_HD;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int r = 0; r < nrows; r++) {
+        const int gi = rows[r];
+        const int pos = off + gi < n_kv - 1 ? off + gi : n_kv - 1;
+        double q[RT4O_HD], O[RT4O_HD];
+        for (int d = 0; d < RT4O_HD; d++) q[d] = fa_q(Q, Qs, n_q, gi, d);
+        double* s = (double*)malloc(sizeof(double) * (size_t)(pos + 1));
+        for (int j = 0; j <= pos; j++) {
+            double acc = 0.0;
+            for (int d = 0; d < RT4O_HD; d++) acc += q[d] * fa_k(K, Ks, kv_cap, j, d);
+            s[j] = acc;
+        }
+        double* o = out + (size_t)r * RT4O_HD;
+        if (mode == 0) {
+            double mx = -1e300, sum = 0.0;
+            for (int j = 0; j <= pos; j++) mx = s[j] > mx ? s[j] : mx;
+            for (int d = 0; d < RT4O_HD; d++) O[d] = 0.0;
+            for (int j = 0; j <= pos; j++) {
+                const double p = exp(s[j] - mx);
+                sum += p;
+                for (int d = 0; d < RT4O_HD; d++) O[d] += p * fa_v(V, Vs, j, d);
+            }
+            for (int d = 0; d < RT4O_HD; d++) o[d] = O[d] / sum;
+        } else {
+            double r_old = -1e300, L = 0.0;
+            for (int d = 0; d < RT4O_HD; d++) O[d] = 0.0;
+            for (int j0 = 0; j0 <= pos; j0 += RT4O_BN) {
+                const int j1 = j0 + RT4O_BN - 1 < pos ? j0 + RT4O_BN - 1 : pos;
+                double mt = -1e300;
+                for (int j = j0; j <= j1; j++) mt = s[j] > mt ? s[j] : mt;
+                double p[RT4O_BN], psum = 0.0;
+                for (int j = j0; j <= j1; j++) {
+                    p[j - j0] = round(7.0 * exp(s[j] - mt));
+                    psum += p[j - j0];
+                }
+                const double r_new = r_old > mt ? r_old : mt;
+                const double alpha = exp(r_old - r_new), beta = exp(mt - r_new) / 7.0;
+                for (int d = 0; d < RT4O_HD; d++) {
+                    double acc = 0.0;
+                    for (int j = j0; j <= j1; j++) acc += p[j - j0] * fa_v(V, Vs, j, d);
+                    O[d] = O[d] * alpha + beta * acc;
+                }
+                L = L * alpha + beta * psum;
+                r_old = r_new;
+            }
+            for (int d = 0; d < RT4O_HD; d++) o[d] = O[d] / L;
+        }
+        free(s);
     }
 }

@@ -39,6 +39,10 @@ def lib() -> ctypes.CDLL:
             "rt4o_make_group_major": ([P, I, I, P], None),
             "rt4o_f32_to_f16_conv": ([ctypes.c_float], ctypes.c_uint16),
             "rt4o_quant_weight_rows": ([P, I, I, P, P], None),
+            "rt4o_attn_q_quant": ([P, P, P, I, I, I, I, I], None),
+            "rt4o_kv_append_k": ([P, P, P, I, I, I, I, I, I], None),
+            "rt4o_kv_append_v": ([P, P, P, P, I, I, I, I, I, I], None),
+            "rt4o_fa_rows": ([P, P, P, P, P, P, I, I, I, I, I, I, P, I, I, P], None),
             "rt4o_gemv_groupsums": ([P, P, I, I, I, P], None),
             "rt4o_gemv_fold": ([P, P, P, I, I, I, P], None),
             "rt4o_gemv_w4a8": ([P, P, P, I, I, I, P], None),
@@ -198,3 +202,49 @@ def gemm_w4a4_points(wq, sb, aq, sa, M, N, K, mi, ni):
     lib().rt4o_gemm_w4a4_points(_p(_c(wq, np.uint32)), _p(_c(sb, np.float32)), _p(_c(aq, np.uint32)),
                                 _p(_c(sa, np.float32)), M, N, K, _p(mi), _p(ni), P, _p(c), _p(Ig))
     return c, Ig
+
+
+# ------------------------------------------------------------ attention --
+HD, BN = 256, 64
+
+
+def attn_q_quant(x: np.ndarray, TP: int, G: int = GROUP, qq=None, qs=None):
+    """attn_q_quant_k (src/k_new.hip:228-253): x f32 [T, H, D] -> (qq uint32 [H, TP, D/8],
+    qs f32 [H, D/G, TP]); rows >= T keep the contents of the passed-in buffers (zeros/ones)."""
+    x = _c(x, np.float32)
+    T, H, D = x.shape
+    if qq is None:
+        qq = np.zeros((H, TP, D // 8), np.uint32)
+    if qs is None:
+        qs = np.ones((H, D // G, TP), np.float32)
+    lib().rt4o_attn_q_quant(_p(qq), _p(qs), _p(x), T, H, D, G, TP)
+    return qq, qs
+
+
+def kv_append_k(kc: np.ndarray, ksc: np.ndarray, kf: np.ndarray, t0: int, G: int = GROUP):
+    """kv_append_k_k (src/k_new.hip:327-347), in place: kc uint32 [H, kv_total, D/8],
+    ksc f32 [H, D/G, kv_total]; kf f32 [T, H, D] written at keys t0..t0+T-1."""
+    kf = _c(kf, np.float32)
+    T, H, D = kf.shape
+    lib().rt4o_kv_append_k(_p(kc), _p(ksc), _p(kf), t0, T, H, D, G, kc.shape[1])
+
+
+def kv_append_v(vc: np.ndarray, vsc: np.ndarray, stage: np.ndarray, vf: np.ndarray, t0: int, kv_total: int):
+    """kv_append_v_k (src/k_new.hip:351-392), in place: vc uint32 [H, kv_total/8, D],
+    vsc f32 [H, kv_total/BG, D], stage f32 [H, BG, D]; vf f32 [T, H, D]."""
+    vf = _c(vf, np.float32)
+    T, H, D = vf.shape
+    BG = stage.shape[1]
+    lib().rt4o_kv_append_v(_p(vc), _p(vsc), _p(stage), _p(vf), t0, T, H, D, BG, kv_total)
+
+
+def fa_rows(qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, kv_cap, ratio, head, rows, mode):
+    """fp64 attention outputs of query rows `rows` of q head `head`: mode 0 = exact softmax
+    (ref_rows, kernels/flash_attn_int4.hip:146-170), mode 1 = the kernel's fixed-point
+    algorithm (ref_alg, :175-217).  -> f64 [len(rows), 256]."""
+    rows = _c(rows, np.int32)
+    out = np.empty((rows.size, HD), np.float64)
+    lib().rt4o_fa_rows(_p(_c(qq, np.uint32)), _p(_c(qsc, np.float32)), _p(_c(kc, np.uint32)),
+                       _p(_c(ksc, np.float32)), _p(_c(vc, np.uint32)), _p(_c(vsc, np.float32)),
+                       n_q, n_kv, off, kv_cap, ratio, head, _p(rows), rows.size, mode, _p(out))
+    return out

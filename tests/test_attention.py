@@ -1,0 +1,354 @@
+"""int4-KV FlashAttention prefill and its feeders (attention row of the RT4 path).
+
+Oracle: oracle/rt4_oracle.c -- the feeders restated bit for bit (src/k_new.hip:
+228-399), the kernel's fixed-point algorithm in fp64 (ref_alg,
+kernels/flash_attn_int4.hip:175-217) and the exact softmax over the same
+quantized values (ref_rows, :146-170).
+
+CPU tests pin the oracle: numpy restatements of the feeders and of the exact
+softmax, a numpy restatement of the tile algorithm, the split-append
+invariance of the V stage, and a case where the fixed-point algorithm is exact.
+
+GPU tests: feeders bit-exact against the oracle and against the reference's
+own feeder kernels built for gfx950; the prefill kernel against the algorithm
+model (rel. L2 < 1e-4: the same algorithm in fp32, where an fp32 score may
+round a P code differently than fp64 does) on edge shapes and on sampled rows
+of the full configs[4] shape.  Against the exact softmax the algorithm itself
+deviates (int4 P): the kernel's deviation must equal the algorithm model's.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from rt4_amd import workload
+
+HD, BN = 256, 64
+
+
+# ------------------------------------------------------------------ helpers --
+
+def nibbles(w: np.ndarray) -> np.ndarray:
+    """uint32 [..., n] -> int codes [..., n, 8] (low nibble first, two's complement)."""
+    nib = (w[..., None].astype(np.uint32) >> (4 * np.arange(8, dtype=np.uint32))) & 0xF
+    return np.where(nib >= 8, nib.astype(np.int64) - 16, nib.astype(np.int64))
+
+
+def np_quant4(x: np.ndarray, G: int):
+    """s = amax/7 per G-group (fp32 division), codes = clip(rint(x/s)) -- lrintf semantics."""
+    xg = x.reshape(*x.shape[:-1], -1, G)
+    amax = np.abs(xg).max(-1)
+    s = np.where(amax > 0, (amax / np.float32(7.0)).astype(np.float32), np.float32(1.0)).astype(np.float32)
+    c = np.clip(np.rint((xg / s[..., None]).astype(np.float32)), -8, 7).astype(np.int64)
+    return c.reshape(x.shape), s
+
+
+def pack8(c: np.ndarray) -> np.ndarray:
+    c = (c.astype(np.int64) & 0xF).astype(np.uint32).reshape(*c.shape[:-1], -1, 8)
+    return np.bitwise_or.reduce(c << (4 * np.arange(8, dtype=np.uint32)), axis=-1).astype(np.uint32)
+
+
+def build_cache(orc, q, k, v, TP, kv_cap):
+    T, H, D = q.shape
+    n_kv, KVH, _ = k.shape
+    qq, qs = orc.attn_q_quant(q, TP)
+    kc = np.zeros((KVH, kv_cap, D // 8), np.uint32)
+    ksc = np.ones((KVH, D // 128, kv_cap), np.float32)
+    orc.kv_append_k(kc, ksc, k, 0)
+    vc = np.zeros((KVH, kv_cap // 8, D), np.uint32)
+    vsc = np.ones((KVH, kv_cap // BN, D), np.float32)
+    stage = np.zeros((KVH, BN, D), np.float32)
+    orc.kv_append_v(vc, vsc, stage, v, 0, kv_cap)
+    return qq, qs, kc, ksc, vc, vsc, stage
+
+
+def dequant(qq, qs, kc, ksc, vc, vsc, head, ratio):
+    vh = head // ratio
+    Q = nibbles(qq[head]).reshape(qq.shape[1], HD) * np.repeat(qs[head].T, 128, axis=1)
+    K = nibbles(kc[vh]).reshape(kc.shape[1], HD) * np.repeat(ksc[vh].T, 128, axis=1)
+    Vcode = nibbles(vc[vh]).transpose(0, 2, 1).reshape(-1, HD)        # [kv/8, D, 8] -> [kv, D]
+    V = Vcode * np.repeat(vsc[vh], BN, axis=0)
+    return Q, K, V
+
+
+def small_case(seed=3, n_q=64, n_kv=320, H=2, KVH=1, scale=True):
+    rng = np.random.default_rng(seed)
+    q, k, v = workload.attn_np(rng, n_q, n_kv, H, KVH)
+    if not scale:
+        q = q * np.float32(16.0)
+    return q, k, v
+
+
+# ------------------------------------------------------------------ CPU side --
+
+def test_feeders_match_numpy(orc):
+    q, k, v = small_case(n_q=48, n_kv=200)
+    q[5, 1, :128] = 0.0                                   # zero group -> s = 1
+    qq, qs = orc.attn_q_quant(q, 64)
+    c, s = np_quant4(q, 128)
+    assert np.array_equal(qq[:, :48], pack8(c).transpose(1, 0, 2))
+    assert np.array_equal(qs[:, :, :48], s.transpose(1, 2, 0))
+    assert np.all(qq[:, 48:] == 0) and np.all(qs[:, :, 48:] == 1.0)       # rows >= T untouched
+    assert qs[1, 0, 5] == 1.0
+    kc = np.zeros((1, 256, 32), np.uint32)
+    ksc = np.ones((1, 2, 256), np.float32)
+    orc.kv_append_k(kc, ksc, k, 0)
+    c, s = np_quant4(k, 128)
+    assert np.array_equal(kc[:, :200], pack8(c).transpose(1, 0, 2))
+    assert np.array_equal(ksc[:, :, :200], s.transpose(1, 2, 0))
+
+
+def test_v_append_tiles_and_split_invariance(orc):
+    _, _, v = small_case(n_kv=200)
+    cap = 256
+    one = [np.zeros((1, cap // 8, HD), np.uint32), np.ones((1, cap // BN, HD), np.float32),
+           np.zeros((1, BN, HD), np.float32)]
+    orc.kv_append_v(*one, v, 0, cap)
+    two = [np.zeros((1, cap // 8, HD), np.uint32), np.ones((1, cap // BN, HD), np.float32),
+           np.zeros((1, BN, HD), np.float32)]
+    for a, b in ((0, 37), (37, 100), (100, 101), (101, 200)):          # appends crossing tiles
+        orc.kv_append_v(*two, v[a:b], a, cap)
+    assert np.array_equal(one[0], two[0]) and np.array_equal(one[1], two[1])
+    # each tile is the per-(tile, dim) quantization of its valid keys, zero codes after
+    for t in range(4):
+        blk = np.zeros((BN, HD), np.float32)
+        n = max(0, min(200 - BN * t, BN))
+        blk[:n] = v[BN * t:BN * t + n, 0]
+        amax = np.abs(blk[:n]).max(0) if n else np.zeros(HD, np.float32)
+        s = np.where(amax > 0, amax / np.float32(7.0), np.float32(1.0)).astype(np.float32)
+        if n == 0:
+            continue
+        c = np.clip(np.rint(blk / s), -8, 7).astype(np.int64)
+        c[n:] = 0
+        assert np.array_equal(one[1][0, t], s)
+        got = nibbles(one[0][0, 8 * t:8 * t + 8]).transpose(0, 2, 1).reshape(BN, HD)
+        assert np.array_equal(got, c)
+
+
+def test_exact_softmax_oracle_matches_numpy(orc):
+    q, k, v = small_case()
+    n_q, n_kv, ratio = 64, 320, 2
+    qq, qs, kc, ksc, vc, vsc, _ = build_cache(orc, q, k, v, n_q, n_kv)
+    off = n_kv - n_q
+    rows = np.arange(n_q, dtype=np.int32)
+    for head in (0, 1):
+        got = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, off, n_kv, ratio, head, rows, 0)
+        Q, K, V = dequant(qq, qs, kc, ksc, vc, vsc, head, ratio)
+        S = Q @ K.T
+        mask = np.arange(n_kv)[None, :] > (off + rows)[:, None]
+        S[mask] = -np.inf
+        P = np.exp(S - S.max(1, keepdims=True))
+        ref = (P @ V) / P.sum(1, keepdims=True)
+        assert rel_l2(got, ref) < 1e-12
+
+
+def np_tile_algorithm(Q, K, V, rows, off, n_kv):
+    """The fixed-point online softmax of fa_int4, written out in numpy (fp64)."""
+    out = []
+    for i in rows:
+        pos = min(off + i, n_kv - 1)
+        s = K[:pos + 1] @ Q[i]
+        O, L, r = np.zeros(HD), 0.0, -np.inf
+        for j0 in range(0, pos + 1, BN):
+            st = s[j0:pos + 1][:BN]
+            mt = st.max()
+            p = np.floor(7.0 * np.exp(st - mt) + 0.5)
+            rn = max(r, mt)
+            a, b = np.exp(r - rn), np.exp(mt - rn) / 7.0
+            O = O * a + b * (p @ V[j0:j0 + len(st)])
+            L = L * a + b * p.sum()
+            r = rn
+        out.append(O / L)
+    return np.array(out)
+
+
+def test_algorithm_oracle_matches_numpy_restatement(orc):
+    for scale in (True, False):
+        q, k, v = small_case(seed=5, scale=scale)
+        n_q, n_kv, ratio = 64, 320, 2
+        qq, qs, kc, ksc, vc, vsc, _ = build_cache(orc, q, k, v, n_q, n_kv)
+        off = n_kv - n_q
+        rows = np.arange(0, n_q, 3, dtype=np.int32)
+        got = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, off, n_kv, ratio, 1, rows, 1)
+        Q, K, V = dequant(qq, qs, kc, ksc, vc, vsc, 1, ratio)
+        assert rel_l2(got, np_tile_algorithm(Q, K, V, rows, off, n_kv)) < 1e-12
+
+
+def test_algorithm_is_exact_when_scores_are_equal(orc):
+    """Q = 0: every visible score is 0, P = 7 everywhere, the fixed-point algorithm
+    reduces to the plain mean of the visible V rows = the exact softmax."""
+    q, k, v = small_case(seed=6)
+    q[:] = 0.0
+    n_q, n_kv = 64, 320
+    qq, qs, kc, ksc, vc, vsc, _ = build_cache(orc, q, k, v, n_q, n_kv)
+    rows = np.arange(n_q, dtype=np.int32)
+    e = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, n_kv - n_q, n_kv, 2, 0, rows, 0)
+    a = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, n_kv - n_q, n_kv, 2, 0, rows, 1)
+    assert rel_l2(a, e) < 1e-13
+
+
+def test_algorithm_error_vs_exact_is_the_reference_scheme(orc):
+    """The int4-P scheme's own distance from the exact softmax: small for sharp
+    softmax (unscaled scores, the reference harness's data: ~1e-2 at 5 tiles and
+    ~2e-3 at 64 tiles, kernels/flash_attn_int4.hip:330-395), large for the flat
+    softmax of 1/sqrt(D)-scaled queries.  Recorded, not a kernel property."""
+    out = {}
+    for scale, n_kv in ((False, 320), (False, 4096), (True, 4096)):
+        q, k, v = small_case(seed=7, n_kv=n_kv, scale=scale)
+        qq, qs, kc, ksc, vc, vsc, _ = build_cache(orc, q, k, v, 64, n_kv)
+        rows = np.arange(0, 64, 9, dtype=np.int32)
+        e = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, 64, n_kv, n_kv - 64, n_kv, 2, 0, rows, 0)
+        a = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, 64, n_kv, n_kv - 64, n_kv, 2, 0, rows, 1)
+        out[(scale, n_kv)] = rel_l2(a, e)
+    assert out[(False, 4096)] < out[(False, 320)] < 0.05
+    assert out[(False, 4096)] < 5e-3
+    assert out[(True, 4096)] > 0.05
+
+
+# ------------------------------------------------------------------ GPU side --
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def gpu_cache(rt4, torch, q, k, v, TP, kv_cap, steps=None):
+    T, H, D = q.shape
+    n_kv, KVH, _ = k.shape
+    qq, qs = rt4.attn_q_quant(dev(torch, q), TP)
+    kc = torch.zeros((KVH, kv_cap, D // 8), dtype=torch.int32, device="cuda")
+    ksc = torch.ones((KVH, D // 128, kv_cap), dtype=torch.float32, device="cuda")
+    vc = torch.zeros((KVH, kv_cap // 8, D), dtype=torch.int32, device="cuda")
+    vsc = torch.ones((KVH, kv_cap // BN, D), dtype=torch.float32, device="cuda")
+    stage = torch.zeros((KVH, BN, D), dtype=torch.float32, device="cuda")
+    kd, vd = dev(torch, k), dev(torch, v)
+    for a, b in (steps or [(0, n_kv)]):
+        rt4.kv_append_k(kc, ksc, kd[a:b].contiguous(), a)
+        rt4.kv_append_v(vc, vsc, stage, vd[a:b].contiguous(), a)
+    torch.cuda.synchronize()
+    return qq, qs, kc, ksc, vc, vsc, stage
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,n_kv,H,KVH,steps", [(48, 200, 3, 1, [(0, 37), (37, 100), (100, 200)]),
+                                                (64, 1024, 24, 4, [(0, 1024)]),
+                                                (5, 4096, 6, 2, [(0, 4000), (4000, 4096)])])
+def test_feeders_bit_exact(rt4, orc, torch_gpu, T, n_kv, H, KVH, steps):
+    print(f"case feeders T={T} n_kv={n_kv} H={H} KVH={KVH}", flush=True)
+    rng = np.random.default_rng(11)
+    q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    q[0, 0, :128] = 0.0
+    TP = (T + 63) // 64 * 64
+    cap = (n_kv + 63) // 64 * 64
+    g = gpu_cache(rt4, torch_gpu, q, k, v, TP, cap, steps)
+    c = [np.zeros((H, TP, 32), np.uint32), np.ones((H, 2, TP), np.float32)]
+    orc.attn_q_quant(q, TP, qq=c[0], qs=c[1])
+    kc = np.zeros((KVH, cap, 32), np.uint32)
+    ksc = np.ones((KVH, 2, cap), np.float32)
+    vc = np.zeros((KVH, cap // 8, HD), np.uint32)
+    vsc = np.ones((KVH, cap // BN, HD), np.float32)
+    st = np.zeros((KVH, BN, HD), np.float32)
+    for a, b in steps:
+        orc.kv_append_k(kc, ksc, k[a:b], a)
+        orc.kv_append_v(vc, vsc, st, v[a:b], a, cap)
+    for got, want in zip(g, (c[0], c[1], kc, ksc, vc, vsc, st)):
+        assert np.array_equal(host(got).view(want.dtype), want)
+
+
+@pytest.mark.gpu
+def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
+    """The reference's own k_attn_q_quant / k_kv_append_k / k_kv_append_v built for gfx950."""
+    print("case feeders vs reference kernels", flush=True)
+    import ctypes
+    torch = torch_gpu
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for fn, args in (("ref_attn_q_quant", [ctypes.c_void_p] * 3 + [ctypes.c_int] * 5),
+                     ("ref_kv_append_k", [ctypes.c_void_p] * 3 + [ctypes.c_int] * 6),
+                     ("ref_kv_append_v", [ctypes.c_void_p] * 4 + [ctypes.c_int] * 6)):
+        getattr(ref_hip, fn).argtypes = args
+        getattr(ref_hip, fn).restype = None
+    rng = np.random.default_rng(12)
+    T, n_kv, H, KVH = 100, 700, 6, 2
+    q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    TP, cap = 128, 704
+    steps = [(0, 333), (333, 334), (334, 700)]
+    ours = gpu_cache(rt4, torch, q, k, v, TP, cap, steps)
+    qq = torch.zeros((H, TP, 32), dtype=torch.int32, device="cuda")
+    qs = torch.ones((H, 2, TP), dtype=torch.float32, device="cuda")
+    ref_hip.ref_attn_q_quant(P(qq), P(qs), P(dev(torch, q)), T, H, HD, 128, TP)
+    kc = torch.zeros((KVH, cap, 32), dtype=torch.int32, device="cuda")
+    ksc = torch.ones((KVH, 2, cap), dtype=torch.float32, device="cuda")
+    vc = torch.zeros((KVH, cap // 8, HD), dtype=torch.int32, device="cuda")
+    vsc = torch.ones((KVH, cap // BN, HD), dtype=torch.float32, device="cuda")
+    st = torch.zeros((KVH, BN, HD), dtype=torch.float32, device="cuda")
+    kd, vd = dev(torch, k), dev(torch, v)
+    for a, b in steps:
+        ref_hip.ref_kv_append_k(P(kc), P(ksc), P(kd[a:b].contiguous()), a, b - a, KVH, HD, 128, cap)
+        ref_hip.ref_kv_append_v(P(vc), P(vsc), P(st), P(vd[a:b].contiguous()), a, b - a, KVH, HD, BN, cap)
+    ref_hip.ref_sync()
+    for got, want in zip(ours, (qq, qs, kc, ksc, vc, vsc, st)):
+        assert torch.equal(got, want)
+
+
+def check_attention(rt4, orc, torch, q, k, v, ratio, off, n_kv, kv_cap, rows_per_head, heads):
+    T, H, _ = q.shape
+    TP = (T + 63) // 64 * 64
+    g = gpu_cache(rt4, torch, q, k, v, TP, kv_cap)
+    out = rt4.attention_prefill(*g[:6], n_kv=n_kv, off=off, ratio=ratio)
+    torch.cuda.synchronize()
+    out = host(out)
+    c = [host(t).view(np.uint32) if t.dtype == torch.int32 else host(t) for t in g[:6]]
+    worst = 0.0
+    for h in heads:
+        rows = rows_per_head(h)
+        alg = orc.fa_rows(*c, TP, n_kv, off, kv_cap, ratio, h, rows, 1)
+        exact = orc.fa_rows(*c, TP, n_kv, off, kv_cap, ratio, h, rows, 0)
+        got = out[h, rows].astype(np.float64)
+        e_alg = rel_l2(got, alg)
+        e_exact, a_exact = rel_l2(got, exact), rel_l2(alg, exact)
+        print(f"  head {h}: kernel vs algorithm {e_alg:.2e}; vs exact {e_exact:.3e} (algorithm itself {a_exact:.3e})")
+        assert e_alg < 1e-4
+        assert abs(e_exact - a_exact) <= 1e-4 + 0.01 * a_exact
+        worst = max(worst, e_alg)
+    return out, worst
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,n_kv,off,H,KVH,cap,scale", [
+    (64, 64, 0, 2, 1, 64, False),          # one tile, square causal
+    (64, 320, 256, 2, 1, 320, False),      # the reference harness's check shape family
+    (128, 200, 72, 4, 2, 256, True),       # n_kv not a multiple of 64, kv_cap > n_kv
+    (192, 1000, 808, 6, 1, 1024, True),    # ratio 6, partial last tile
+    (64, 2048, 1984, 1, 1, 4096, False),   # no GQA, long-ish
+])
+def test_attention_against_oracle(rt4, orc, torch_gpu, T, n_kv, off, H, KVH, cap, scale):
+    print(f"case attention T={T} n_kv={n_kv} off={off} H={H} KVH={KVH} cap={cap}", flush=True)
+    rng = np.random.default_rng(13)
+    q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    if not scale:
+        q = q * np.float32(16.0)
+    ratio = H // KVH
+    all_rows = np.arange(T, dtype=np.int32)
+    check_attention(rt4, orc, torch_gpu, q, k, v, ratio, off, n_kv, cap, lambda h: all_rows, range(H))
+
+
+@pytest.mark.gpu
+def test_attention_benchmark_shape_sampled(rt4, orc, torch_gpu):
+    """24 heads, GQA 6:1, 1024 queries over a 32768-token cache."""
+    c4 = workload.ATTN_C4
+    n_q, ctx = c4["n_q"], c4["ctx"]
+    n_kv = ctx + n_q
+    print(f"case attention C4 n_q={n_q} n_kv={n_kv}", flush=True)
+    rng = np.random.default_rng(14)
+    q, k, v = workload.attn_np(rng, n_q, n_kv, c4["H"], c4["KVH"])
+    rows = np.array([0, 1, 63, 64, 511, 1000, 1023], np.int32)
+    out, _ = check_attention(rt4, orc, torch_gpu, q, k, v, c4["H"] // c4["KVH"], ctx, n_kv, n_kv,
+                             lambda h: rows, (0, 5, 6, 23))
+    assert np.isfinite(out).all()
