@@ -168,6 +168,16 @@ int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, cons
                           const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv,
                           int off, int n_tile, int n_heads, int ratio, int kv_cap, void* stream);
 
+/* Same, with an explicit number of KV splits per (64-row query block, head)
+ * (tuning and tests; 0 selects the default that balances the grid over the
+ * device's CUs).  With more than one split each split writes its partial state
+ * (unnormalised output, running max, denominator) to library scratch (grown
+ * with hipMalloc) and a second kernel combines the splits in order. */
+int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
+                              const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv,
+                              int off, int n_tile, int n_heads, int ratio, int kv_cap, int kv_splits,
+                              void* stream);
+
 /* ------------------------------------------- W4A4 siblings (link only) ---- */
 
 /* int4 activation quantizer.  Replaces k_quant_rows (src/kernels.h:36,

@@ -47,6 +47,8 @@ constexpr int BNK = 64;           // keys per tile
 constexpr int QROWS = 64;         // query rows per workgroup
 constexpr int NTA = 256;          // 4 waves
 constexpr float L2E = 1.4426950408889634f;
+constexpr int KU_BYTES = 4 * 4 * 64 * 16;   // unpacked K operands of one tile
+constexpr int VU_BYTES = 16 * 64 * 16;      // unpacked V operands of one tile
 
 __device__ __forceinline__ int sext4(uint32_t w, int e) { return ((int)(w << (28 - 4 * e))) >> 28; }
 
@@ -169,11 +171,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                                                     const uint32_t* __restrict__ vc,
                                                     const float* __restrict__ vsc, float* __restrict__ out,
                                                     int n_q, int n_kv, int off, int n_tile, int ratio,
-                                                    int kv_cap) {
-    __shared__ __align__(16) unsigned char ku[4 * 4 * 64 * 16];   // [subtile][k-step][lane] x 16 B
-    __shared__ __align__(16) unsigned char vu[16 * 64 * 16];      // [dim tile][lane] x 16 B
-    __shared__ __align__(16) float ks_l[2 * BNK];
-    __shared__ __align__(16) float vs_l[HD];
+                                                    int kv_cap, int nsplit, float* __restrict__ opart,
+                                                    float2* __restrict__ mlpart) {
+    __shared__ __align__(16) unsigned char ku[2 * KU_BYTES];   // x2: [subtile][k-step][lane] x 16 B
+    __shared__ __align__(16) unsigned char vu[2 * VU_BYTES];   // x2: [dim tile][lane] x 16 B
+    __shared__ __align__(16) float ks_l[2][2 * BNK];
+    __shared__ __align__(16) float vs_l[2][HD];
 
     const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
     const int qi = lane & 15, G = lane >> 4;
@@ -191,6 +194,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // tiles holding keys at or before this workgroup's last query position
     int nt = (off + q0 + QROWS - 1) / BNK + 1;
     nt = nt < n_tile ? nt : n_tile;
+    // split-KV: this workgroup takes tiles [t0, t1) of them
+    const int split = blockIdx.z;
+    const int t0 = (int)((long long)nt * split / nsplit), t1 = (int)((long long)nt * (split + 1) / nsplit);
 
     // resident Q operand: k-step s covers dims 64s + 16G .. +15 (dwords 8s+2G, 8s+2G+1)
     v4i qop[4];
@@ -210,49 +216,61 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         for (int r = 0; r < 4; r++) O[dt][r] = 0.f;
     float rref = -1e30f, L = 0.f;
 
-    // staging registers: K rows (key tid%64, k-step tid/64: 8 dwords), V (dim tid: 8 key groups)
-    uint4 kr0, kr1;
-    uint32_t vr[8];
-    float ksr = 1.f, vsr = 1.f;
-    auto load_tile = [&](int t) {
+    // Pipeline: one register set stages the packed K/V of the next tile (its
+    // global loads are in flight during a whole tile of compute) and two LDS
+    // buffers hold unpacked operands (one read by the tile being computed, one
+    // written with the next tile), so each tile costs one barrier.
+    struct Stage {
+        uint4 k0, k1;                   // key tid%64, dwords 8p..8p+7 (p = tid/64)
+        uint32_t v[8];                  // dim tid, 8-key groups 0..7
+        float ks, vs;
+    };
+    // Branch-free loads with addresses clamped into the cache; the out-of-range
+    // values are replaced (zero codes, unit scales) only when the stage is
+    // unpacked.  Selecting right after a load, or loading under a condition, makes
+    // the compiler wait for the load there, which would defeat the prefetch.
+    auto load = [&](Stage& S, int t) {
         const int kb = t * BNK;
         const int kk = tid & 63, p = tid >> 6;
-        if (kb + kk < n_kv) {
-            const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)(kb + kk) * KDW + 8 * p);
-            kr0 = src[0];
-            kr1 = src[1];
-        } else {
-            kr0 = make_uint4(0, 0, 0, 0);
-            kr1 = kr0;
-        }
+        const int krow = kb + kk < n_kv ? kb + kk : 0;
+        const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)krow * KDW + 8 * p);
+        S.k0 = src[0];
+        S.k1 = src[1];
 #pragma unroll
         for (int g = 0; g < 8; g++) {
-            const int k8 = kb / 8 + g;   // a group of 8 keys is read only if it is whole (flash_attn_core.h:150)
-            vr[g] = ((size_t)k8 * 8 + 8 <= (size_t)n_kv) ? vc[(size_t)k8 * HD + tid] : 0u;
+            const int k8 = kb / 8 + g;
+            S.v[g] = vc[(size_t)(k8 * 8 + 8 <= n_kv ? k8 : 0) * HD + tid];
         }
-        if (tid < 2 * BNK) {
-            const int g = tid / BNK, j = kb + (tid % BNK);
-            ksr = j < kv_cap ? ksc[(size_t)g * kv_cap + j] : 1.f;
-        }
-        vsr = (t < kv_cap / BNK) ? vsc[(size_t)t * HD + tid] : 1.f;
+        const int j = kb + (tid & 63);
+        S.ks = ksc[(size_t)((tid >> 6) & 1) * kv_cap + (tid < 2 * BNK && j < kv_cap ? j : 0)];
+        S.vs = vsc[(size_t)(t < kv_cap / BNK ? t : 0) * HD + tid];
     };
-    auto store_tile = [&]() {
-        {   // K: x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16
+    auto store = [&](const Stage& S, int b, int t) {
+        const int kb = t * BNK;
+        unsigned char* kub = ku + b * KU_BYTES;
+        unsigned char* vub = vu + b * VU_BYTES;
+        {   // K: x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16;
+            // keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
             const int kk = tid & 63, p = tid >> 6;
-            const uint32_t d[8] = {kr0.x, kr0.y, kr0.z, kr0.w, kr1.x, kr1.y, kr1.z, kr1.w};
+            const bool kin = kb + kk < n_kv;
+            uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
+#pragma unroll
+            for (int g = 0; g < 8; g++) d[g] = kin ? d[g] : 0u;
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
                                            odd_x16(d[2 * g + 1]));
-                *reinterpret_cast<uint4*>(ku + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
+                *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
             }
         }
         {   // V: lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3
+            // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
             uint32_t e[8], o[8];
 #pragma unroll
             for (int g = 0; g < 8; g++) {
-                e[g] = even_x16(vr[g]);
-                o[g] = odd_x16(vr[g]);
+                const uint32_t v = (kb / 8 + g) * 8 + 8 <= n_kv ? S.v[g] : 0u;
+                e[g] = even_x16(v);
+                o[g] = odd_x16(v);
             }
 #pragma unroll
             for (int g = 0; g < 4; g++) {
@@ -262,33 +280,31 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 v.y = __builtin_amdgcn_perm(o[2 + (g >> 1)], e[2 + (g >> 1)], sel);
                 v.z = __builtin_amdgcn_perm(o[4 + (g >> 1)], e[4 + (g >> 1)], sel);
                 v.w = __builtin_amdgcn_perm(o[6 + (g >> 1)], e[6 + (g >> 1)], sel);
-                *reinterpret_cast<uint4*>(vu + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
+                *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
             }
         }
-        if (tid < 2 * BNK) ks_l[tid] = ksr;
-        vs_l[tid] = vsr;
+        if (tid < 2 * BNK) ks_l[b][tid] = kb + (tid & 63) < kv_cap ? S.ks : 1.f;
+        vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
     };
 
     const v4i zero = {0, 0, 0, 0};
-    if (nt > 0) load_tile(0);
-    for (int t = 0; t < nt; t++) {
+    auto compute = [&](int t, int b) {
         const int kb = t * BNK;
-        __syncthreads();                 // the previous tile's operands are no longer read
-        store_tile();
-        __syncthreads();
-        if (t + 1 < nt) load_tile(t + 1);
-
+        const unsigned char* kub = ku + b * KU_BYTES;
+        const unsigned char* vub = vu + b * VU_BYTES;
+        const float* ksb = ks_l[b];
+        const float* vsb = vs_l[b];
         // ---- S^T = K Q^T for the 4 subtiles of 16 keys
         float sv[4][4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
-            const v4i* kp = reinterpret_cast<const v4i*>(ku) + (kt * 4) * 64 + lane;
+            const v4i* kp = reinterpret_cast<const v4i*>(kub) + (kt * 4) * 64 + lane;
             v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[0], qop[0], zero, 0, 0, 0);
             a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[64], qop[1], a0, 0, 0, 0);
             v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
             a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
-            const float4 k0 = *reinterpret_cast<const float4*>(ks_l + 16 * kt + 4 * G);
-            const float4 k1 = *reinterpret_cast<const float4*>(ks_l + BNK + 16 * kt + 4 * G);
+            const float4 k0 = *reinterpret_cast<const float4*>(ksb + 16 * kt + 4 * G);
+            const float4 k1 = *reinterpret_cast<const float4*>(ksb + BNK + 16 * kt + 4 * G);
             const float s0[4] = {k0.x, k0.y, k0.z, k0.w}, s1[4] = {k1.x, k1.y, k1.z, k1.w};
 #pragma unroll
             for (int r = 0; r < 4; r++)
@@ -299,7 +315,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -1e30f;
+                    if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -__builtin_inff();
         }
         // ---- tile row max over the 64 keys of this lane's query
         float m = sv[0][0];
@@ -309,7 +325,11 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             for (int r = 0; r < 4; r++) m = fmaxf(m, sv[kt][r]);
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
-        if (m < -1e29f) m = rref;        // fully masked row: alpha = 1, beta folds to nothing
+        // Fully masked row in this tile: take the running reference, so alpha = 1 and
+        // every P is 2^(-inf) = 0.  (The reference masks with -1e30 and reaches this
+        // only after a visible tile; -inf gives the same P there and also keeps a row
+        // that has seen nothing yet -- possible at the start of a KV split -- at zero.)
+        if (m < -1e29f) m = rref;
         // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand
         int isum = 0;
         uint32_t pk[4];
@@ -318,7 +338,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             int pq[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float p = exp2f(sv[kt][r] - m) * 7.f;
+                // v_exp_f32 directly: the arguments are <= 0 and any result below
+                // 2^-4 quantizes to P = 0, so denormal handling is irrelevant here
+                const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m) * 7.f;
                 int q = (int)(p + 0.5f);
                 q = q > 7 ? 7 : (q < 0 ? 0 : q);
                 pq[r] = q;
@@ -337,26 +359,83 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // ---- O^T = V^T P^T, folded per dim tile
         const v4i pop = {(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
         const float pb16 = pb * 0.0625f;          // V is x16 unpacked
-        const bool rescale = !__all(alpha == 1.f);
+        // O * alpha is exact when alpha == 1 (running max unchanged): skip it when
+        // that holds for every row of the wave (a wave-uniform branch)
+        if (!__all(alpha == 1.f)) {
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) O[dt][r] *= alpha;
+        }
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) {
-            const v4i va = *(reinterpret_cast<const v4i*>(vu) + dt * 64 + lane);
+            const v4i va = *(reinterpret_cast<const v4i*>(vub) + dt * 64 + lane);
             const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pop, zero, 0, 0, 0);
-            const float4 s4 = *reinterpret_cast<const float4*>(vs_l + 16 * dt + 4 * G);
+            const float4 s4 = *reinterpret_cast<const float4*>(vsb + 16 * dt + 4 * G);
             const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float o = rescale ? O[dt][r] * alpha : O[dt][r];
-                O[dt][r] = fmaf((float)acc[r], pb16 * sc[r], o);
-            }
+            for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], pb16 * sc[r], O[dt][r]);
         }
+    };
+
+    Stage S;
+    if (t0 < t1) {
+        load(S, t0);
+        store(S, t0 & 1, t0);
+        if (t0 + 1 < t1) load(S, t0 + 1);
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    float* orow = out + (size_t)qrow * HD + 4 * G;
+    __syncthreads();
+    for (int t = t0; t < t1; t++) {
+        // tile t is in LDS buffer t&1; S holds tile t+1 (loaded during the previous
+        // tile): unpack it into the other buffer, start the loads of tile t+2, then
+        // compute tile t.  Storing before computing keeps S's registers free during
+        // the compute phase.
+        if (t + 1 < t1) {
+            store(S, (t + 1) & 1, t + 1);
+            if (t + 2 < t1) load(S, t + 2);
+        }
+        // keep the loads here: left to itself the compiler sinks them next to their
+        // use at the top of the next iteration, exposing their whole latency
+        asm volatile("" ::: "memory");
+        compute(t, t & 1);
+        __syncthreads();
+    }
+    if (nsplit == 1) {
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        float* orow = out + (size_t)qrow * HD + 4 * G;
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++)
-        *reinterpret_cast<float4*>(orow + 16 * dt) =
-            make_float4(O[dt][0] * inv, O[dt][1] * inv, O[dt][2] * inv, O[dt][3] * inv);
+        for (int dt = 0; dt < 16; dt++)
+            *reinterpret_cast<float4*>(orow + 16 * dt) =
+                make_float4(O[dt][0] * inv, O[dt][1] * inv, O[dt][2] * inv, O[dt][3] * inv);
+    } else {
+        // partial state of this split: unnormalised O, running max (log2 units), L
+        const size_t prow = ((size_t)split * gridDim.y + head) * n_q + qrow;
+        float* orow = opart + prow * HD + 4 * G;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+            *reinterpret_cast<float4*>(orow + 16 * dt) = make_float4(O[dt][0], O[dt][1], O[dt][2], O[dt][3]);
+        if (G == 0) mlpart[prow] = make_float2(rref, L);
+    }
+}
+
+// Combine of the KV splits of one (head, query row): with M the largest running
+// max, out = Σ_s O_s 2^(m_s - M) / Σ_s L_s 2^(m_s - M), splits in order.
+// grid (n_q, H), block 256 (one thread per dim).
+__global__ __launch_bounds__(256) void fa_combine_k(float* __restrict__ out, const float* __restrict__ opart,
+                                                   const float2* __restrict__ mlpart, int n_q, int nsplit) {
+    const int row = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+    const int H = gridDim.y;
+    float M = -__builtin_inff();
+    for (int s = 0; s < nsplit; s++) M = fmaxf(M, mlpart[((size_t)s * H + head) * n_q + row].x);
+    float o = 0.f, l = 0.f;
+    for (int s = 0; s < nsplit; s++) {
+        const size_t prow = ((size_t)s * H + head) * n_q + row;
+        const float2 ml = mlpart[prow];
+        const float a = exp2f(ml.x - M);
+        o = fmaf(a, opart[prow * HD + d], o);
+        l = fmaf(a, ml.y, l);
+    }
+    out[((size_t)head * n_q + row) * HD + d] = l > 0.f ? o / l : 0.f;
 }
 
 // -------------------------------------------------------------- launchers --
@@ -397,11 +476,37 @@ hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const floa
     return hipGetLastError();
 }
 
+int fa_splits(int n_q, int n_heads, int n_tile, int cus) {
+    // workgroups resident per CU: LDS (double-buffered operands) allows two
+    const int slots = (cus > 0 ? cus : 256) * 2;
+    const int items = (n_q / QROWS) * n_heads;
+    int best = 1;
+    double best_eff = 0.0;
+    for (int s = 1; s <= 8; s++) {
+        if (s > 1 && n_tile / s < 8) break;          // keep at least 8 tiles per split
+        const long long blocks = (long long)items * s;
+        const double eff = (double)blocks / ((double)slots * (double)((blocks + slots - 1) / slots));
+        if (eff > best_eff + 0.02) {
+            best_eff = eff;
+            best = s;
+        }
+    }
+    return best;
+}
+
+size_t fa_part_bytes(int n_q, int n_heads, int nsplit) {
+    return nsplit > 1 ? (size_t)nsplit * n_heads * n_q * (HD + 2) * sizeof(float) : 0;
+}
+
 hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                           const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
-                          int n_heads, int ratio, int kv_cap, hipStream_t st) {
-    hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc, out,
-                       n_q, n_kv, off, n_tile, ratio, kv_cap);
+                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, hipStream_t st) {
+    float* opart = part;
+    float2* mlpart = part ? reinterpret_cast<float2*>(part + (size_t)nsplit * n_heads * n_q * HD) : nullptr;
+    hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads, nsplit), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc,
+                       out, n_q, n_kv, off, n_tile, ratio, kv_cap, nsplit, opart, mlpart);
+    if (nsplit > 1)
+        hipLaunchKernelGGL(fa_combine_k, dim3(n_q, n_heads), dim3(256), 0, st, out, opart, mlpart, n_q, nsplit);
     return hipGetLastError();
 }
 

@@ -31,7 +31,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // hipFree synchronizes the device, so a buffer still read by queued kernels is
 // never released early.  Not safe for concurrent calls from several threads
 // (the reference's scratch has the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlots = 5 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlots = 6 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -324,21 +324,35 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
                       "k_kv_append_v launch");
 }
 
-int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
-                          const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
-                          int n_tile, int n_heads, int ratio, int kv_cap, void* stream) {
+int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
+                              const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
+                              int n_tile, int n_heads, int ratio, int kv_cap, int kv_splits, void* stream) {
     if (!out || !qq || !qsc || !kc || !ksc || !vc || !vsc) return fail(RT4_E_ARG, "k_attention: null pointer");
     if (n_q < 64 || n_q % 64 || n_kv < 1 || n_kv > kv_cap || off < 0 || kv_cap % 64 || n_tile < 1 ||
-        (long long)n_tile * 64 > kv_cap || n_heads < 1 || ratio < 1 || n_heads % ratio || n_q > 65535 * 64)
+        (long long)n_tile * 64 > kv_cap || n_heads < 1 || ratio < 1 || n_heads % ratio || n_q > 65535 * 64 ||
+        n_heads > 65535)
         return fail(RT4_E_SHAPE,
                     "k_attention: n_q=%d (multiple of 64) n_kv=%d off=%d n_tile=%d n_heads=%d ratio=%d kv_cap=%d",
                     n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap);
+    if (kv_splits < 0 || kv_splits > 64) return fail(RT4_E_ARG, "k_attention: kv_splits=%d (0..64)", kv_splits);
     if (!aligned(qq, 16) || !aligned(kc, 16) || !aligned(vc, 4) || !aligned(out, 16) || !aligned(qsc, 4) ||
         !aligned(ksc, 4) || !aligned(vsc, 4))
         return fail(RT4_E_ARG, "k_attention: misaligned pointer (qq, kc, out need 16 bytes)");
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    const int nsplit = kv_splits > 0 ? kv_splits : rt4::fa_splits(n_q, n_heads, n_tile, cus);
+    void* part = nullptr;
+    if (nsplit > 1 && (rc = scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part))) return rc;
     return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
-                                          kv_cap, as_stream(stream)),
+                                          kv_cap, nsplit, static_cast<float*>(part), as_stream(stream)),
                       "k_attention launch");
+}
+
+int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
+                          const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
+                          int n_tile, int n_heads, int ratio, int kv_cap, void* stream) {
+    return rt4_attention_prefill_cfg(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap,
+                                     0, stream);
 }
 
 }  // extern "C"

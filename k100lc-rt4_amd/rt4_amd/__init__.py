@@ -33,6 +33,7 @@ C_EXPORTS = (
     "rt4_make_group_major", "rt4_quant_rows_a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
     "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
+    "rt4_attention_prefill_cfg",
 )
 # The reference-compatible C++ entry points (include/rt4_kernels.h), mangled.
 CXX_EXPORTS = (
@@ -72,6 +73,7 @@ _SIGS = {
     "rt4_kv_append_k": [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "rt4_kv_append_v": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "rt4_attention_prefill": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_attention_prefill_cfg": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P],
 }
 
 
@@ -307,8 +309,8 @@ def kv_append_v(vc, vsc, stage, vf, t0: int):
 
 
 def attention_prefill(qq, qsc, kc, ksc, vc, vsc, n_kv: int, off: int, ratio: int,
-                      n_tile: int | None = None, out=None):
-    """Prefill branch of k_attention -> out f32 [H, n_q, 256]."""
+                      n_tile: int | None = None, out=None, kv_splits: int = 0):
+    """Prefill branch of k_attention -> out f32 [H, n_q, 256] (kv_splits 0 = automatic)."""
     torch = _torch()
     H, n_q, _ = qq.shape
     kv_cap = kc.shape[1]
@@ -316,6 +318,6 @@ def attention_prefill(qq, qsc, kc, ksc, vc, vsc, n_kv: int, off: int, ratio: int
         n_tile = (n_kv + KV_TILE - 1) // KV_TILE
     if out is None:
         out = torch.empty((H, n_q, HEAD_DIM), dtype=torch.float32, device=qq.device)
-    _check(lib().rt4_attention_prefill(_ptr(out), _ptr(qq), _ptr(qsc), _ptr(kc), _ptr(ksc), _ptr(vc), _ptr(vsc),
-                                       n_q, n_kv, off, n_tile, H, ratio, kv_cap, _stream()))
+    _check(lib().rt4_attention_prefill_cfg(_ptr(out), _ptr(qq), _ptr(qsc), _ptr(kc), _ptr(ksc), _ptr(vc),
+                                           _ptr(vsc), n_q, n_kv, off, n_tile, H, ratio, kv_cap, kv_splits, _stream()))
     return out

@@ -297,13 +297,17 @@ def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
         assert torch.equal(got, want)
 
 
-def check_attention(rt4, orc, torch, q, k, v, ratio, off, n_kv, kv_cap, rows_per_head, heads):
+def check_attention(rt4, orc, torch, q, k, v, ratio, off, n_kv, kv_cap, rows_per_head, heads, splits=(0,)):
     T, H, _ = q.shape
     TP = (T + 63) // 64 * 64
     g = gpu_cache(rt4, torch, q, k, v, TP, kv_cap)
-    out = rt4.attention_prefill(*g[:6], n_kv=n_kv, off=off, ratio=ratio)
+    outs = [host(rt4.attention_prefill(*g[:6], n_kv=n_kv, off=off, ratio=ratio, kv_splits=s)) for s in splits]
     torch.cuda.synchronize()
-    out = host(out)
+    out = outs[0]
+    for s, o in zip(splits[1:], outs[1:]):            # KV splits change only the fp32 rounding
+        e = rel_l2(o, out)
+        print(f"  kv_splits={s}: vs first {e:.2e}")
+        assert e < 1e-5
     c = [host(t).view(np.uint32) if t.dtype == torch.int32 else host(t) for t in g[:6]]
     worst = 0.0
     for h in heads:
@@ -336,7 +340,8 @@ def test_attention_against_oracle(rt4, orc, torch_gpu, T, n_kv, off, H, KVH, cap
         q = q * np.float32(16.0)
     ratio = H // KVH
     all_rows = np.arange(T, dtype=np.int32)
-    check_attention(rt4, orc, torch_gpu, q, k, v, ratio, off, n_kv, cap, lambda h: all_rows, range(H))
+    check_attention(rt4, orc, torch_gpu, q, k, v, ratio, off, n_kv, cap, lambda h: all_rows, range(H),
+                    splits=(0, 1, 2, 3, 7))
 
 
 @pytest.mark.gpu
