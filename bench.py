@@ -12,8 +12,8 @@ in HBM before timing; steps are replayed from a HIP graph (no host launch
 overhead inside the timed region).
 
 value = algorithmic bytes of a step / time per step (GB/s), where the bytes of
-one linear are weights + fp16 scales + int8 activations + activation scales +
-fp32 output (46,257,408 B for gate/up, 46,113,024 B for down).
+one linear are int4 weights + fp16 scales + fp32 activations + fp32 output
+(46,317,568 B for gate/up, 46,222,336 B for down).
 
 Also printed in the same JSON line:
   roofline      the dominant kernel (the gate/up GEMV launch), timed live with
@@ -43,9 +43,17 @@ I8_PEAK_TOPS = 5000.0          # MI355X published dense int8 MFMA
 
 
 def linear_bytes(M: int, N: int, K: int) -> int:
-    """Algorithmic HBM bytes of one W4A8 GEMV call."""
+    """Algorithmic HBM bytes of one drop-in W4A8 linear: weights, their scales, the
+    fp32 activations read once and the fp32 output written once."""
     NG = K // 128
-    return N * K // 2 + N * NG * 2 + M * K + 2 * M * NG * 4 + M * N * 4
+    return N * K // 2 + N * NG * 2 + M * K * 4 + M * N * 4
+
+
+def gemv_kernel_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic HBM bytes of one GEMV launch on quantized activations: weights,
+    their scales, int8 activations and their scales, fp32 output."""
+    NG = K // 128
+    return N * K // 2 + N * NG * 2 + M * K + M * NG * 4 + M * N * 4
 
 
 def parse():
@@ -203,8 +211,8 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
     M, (N, K) = 4, (17408, 5120)
     mats = [workload.weights_torch(N, K, generator=gen) for _ in range(16)]
     x = workload.acts_torch(M, K, generator=gen)
-    xq, sa = rt4_amd.quant_act_a8(x)
     y = torch.empty((M, N), device="cuda")
+    xq, sa = rt4_amd.quant_act_a8(x)
     for _ in range(2):
         for wq, ws in mats:
             rt4_amd.gemv_w4a8_q(wq, ws, xq, sa, out=y)
@@ -302,7 +310,6 @@ def main() -> int:
 
     # ---- dominant kernel: the gate/up GEMV launch, back to back over all layers
     xq_gu, sa_gu = rt4_amd.quant_act_a8(x_gu)
-    xq_d, sa_d = rt4_amd.quant_act_a8(x_d)
     gu_mats = [lw[k] for lw in layers for k in ("gate", "up")]
 
     def gemv_gu():
@@ -310,9 +317,12 @@ def main() -> int:
             rt4_amd.gemv_w4a8_q(wq, ws, xq_gu, sa_gu, out=y_g)
 
     gu_us = timed_graph(torch, gemv_gu) * 1e3 / len(gu_mats)
-    gu_bytes = linear_bytes(M, Ngu, Kgu)
+    gu_bytes = gemv_kernel_bytes(M, Ngu, Kgu)
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    roofline = {"kernel": "rt4::gemv_w4a8_k<4,10,false> (gate/up, M=4 K=5120 N=17408)",
+    plan = rt4_amd.gemv_launch_plan(M, Ngu, Kgu)
+    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{plan['groups_per_wave']},false,false> (gate/up GEMV, "
+                          f"M={M} K={Kgu} N={Ngu}, "
+                          f"{plan['waves']} waves/tile, {plan['k_splits']} K pieces/leftover tile)",
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv_gate_up"),
                 "us_per_launch": round(gu_us, 3), "bytes_per_launch": gu_bytes,
@@ -322,12 +332,21 @@ def main() -> int:
     if not args.no_extra:
         d_mats = [lw["down"] for lw in layers]
 
+        xq_d, sa_d = rt4_amd.quant_act_a8(x_d)
+
         def gemv_d():
             for wq, ws in d_mats:
                 rt4_amd.gemv_w4a8_q(wq, ws, xq_d, sa_d, out=y_d)
 
         d_us = timed_graph(torch, gemv_d) * 1e3 / len(d_mats)
-        kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(linear_bytes(M, Nd, Kd) / d_us / 1e3, 1)}
+        kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(gemv_kernel_bytes(M, Nd, Kd) / d_us / 1e3, 1)}
+
+        def gemv_gu_fused():
+            for wq, ws in gu_mats:
+                rt4_amd.gemv_w4a8(wq, ws, x_gu, out=y_g, groups_per_wave=plan["groups_per_wave"])
+
+        f_gu_us = timed_graph(torch, gemv_gu_fused) * 1e3 / len(gu_mats)
+        kernels["gemv_gate_up_m4_fused_quant"] = {"us": round(f_gu_us, 3)}
 
         def quant_gu():
             for _ in range(16):
@@ -336,8 +355,7 @@ def main() -> int:
         q_us = timed_graph(torch, quant_gu) * 1e3 / 16
         kernels["quant_act_m4_k5120"] = {"us": round(q_us, 3)}
         # M=1 decode (C0 shape 5120x5120) over 16 rotated slices of the gate weights
-        x1 = x_gu[:1].contiguous()
-        xq1, sa1 = rt4_amd.quant_act_a8(x1)
+        xq1, sa1 = rt4_amd.quant_act_a8(x_gu[:1].contiguous())
         c0_mats = [(wq[:5120], ws[:5120]) for wq, ws in gu_mats]
         y1 = torch.empty((1, 5120), device="cuda")
 
@@ -346,7 +364,7 @@ def main() -> int:
                 rt4_amd.gemv_w4a8_q(wq, ws, xq1, sa1, out=y1)
 
         c0_us = timed_graph(torch, gemv_c0) * 1e3 / len(c0_mats)
-        kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(linear_bytes(1, 5120, 5120) / c0_us / 1e3, 1)}
+        kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(gemv_kernel_bytes(1, 5120, 5120) / c0_us / 1e3, 1)}
         # LM head (C3): M=4, K=5120, N=248320, two 0.66 GB copies alternated
         del layers, gu_mats, d_mats, c0_mats
         torch.cuda.empty_cache()
@@ -360,7 +378,7 @@ def main() -> int:
 
         lm_us = timed_graph(torch, gemv_lm) * 1e3 / len(lm)
         kernels["gemv_lm_head_m4"] = {"us": round(lm_us, 3),
-                                      "GBs": round(linear_bytes(M, 248320, 5120) / lm_us / 1e3, 1)}
+                                      "GBs": round(gemv_kernel_bytes(M, 248320, 5120) / lm_us / 1e3, 1)}
         del lm
         torch.cuda.empty_cache()
 

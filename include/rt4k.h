@@ -62,10 +62,20 @@ int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8
 /* Same, with an explicit launch configuration (tuning and tests).  A
  * workgroup owns one 16-row weight tile; groups_per_wave (even, 2..12) is the
  * number of 128-wide K groups each wave streams per pass, waves (1..16, at most
- * the number of such chunks) the waves per workgroup.  0 selects the default. */
+ * the number of such chunks) the waves per workgroup.  When the tile count is
+ * not a multiple of the CU count, the leftover tiles can be cut along K into
+ * pieces that run on otherwise idle CUs: k_splits 1 keeps every tile whole,
+ * S >= 2 allows up to S pieces per leftover tile.  0 selects the default for
+ * each parameter. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
-                        void* stream);
+                        int k_splits, void* stream);
+
+/* The launch configuration rt4_gemv_w4a8_q picks for this shape on the
+ * current device: groups per wave, waves per workgroup and the number of K
+ * pieces per leftover tile (1: all tiles whole).  No counterpart in the
+ * reference (its launch is fixed per M); for tuning and reports. */
+int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits);
 
 /* Test hook: the same kernel, also writing the exact per-group int32 dot
  * products gsum int32 [rows][N][K/128] = Σ_{k∈g} code[n][k]*xq[m][k]. */
@@ -73,13 +83,22 @@ int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const u
                             const int8_t* xq, const float* sa, int rows, int N, int K,
                             void* stream);
 
-/* The whole decode linear: quantize x, then the GEMV.  Replaces k_gemv_w4a8
- * (src/kernels.h:27, src/k_gemv.hip:53-106).  x f32 [rows][K] contiguous.
- * Uses library-owned scratch for the quantized activations, grown with
- * hipMalloc on first use per device (as the reference does, src/k_gemv.hip:
- * 56-67); not re-entrant across threads. */
+/* The whole decode linear: quantize x per (row, 128-group) to int8, then the
+ * GEMV.  Replaces k_gemv_w4a8 (src/kernels.h:27, src/k_gemv.hip:53-106), which
+ * is two launches (quant_act, then the GEMV), as is this one.  x f32
+ * [rows][K] contiguous.  The quantized activations go to library-owned
+ * scratch, grown with hipMalloc on first use per device (as the reference
+ * does, src/k_gemv.hip:56-67); not re-entrant across threads. */
 int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows,
                   int N, int K, void* stream);
+
+/* rt4_gemv_w4a8 as ONE launch, with an explicit launch configuration
+ * (parameters as rt4_gemv_w4a8_q_cfg; tuning and tests): the GEMV's waves
+ * quantize the activations in registers, codes and scales bit-identical to
+ * rt4_quant_act_a8, so y equals the two-launch result bit for bit.  No
+ * library scratch.  x must be 16-byte aligned. */
+int rt4_gemv_w4a8_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
+                      int groups_per_wave, int waves, int k_splits, void* stream);
 
 /* ----------------------------------------------------------- prefill path -- */
 

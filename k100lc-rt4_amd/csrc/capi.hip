@@ -31,7 +31,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // hipFree synchronizes the device, so a buffer still read by queued kernels is
 // never released early.  Not safe for concurrent calls from several threads
 // (the reference's scratch has the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlots = 6 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlots = 8 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -39,6 +39,14 @@ struct Buf {
 };
 std::mutex g_mu;
 Buf g_buf[kMaxDev][kSlots];
+
+// Whether this device's scratch slot already holds at least `bytes`.
+bool scratch_has(Slot slot, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_buf[dev][slot].cap >= bytes;
+}
 
 int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, bool zero = false) {
     int dev = 0;
@@ -122,6 +130,56 @@ int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const
                       who);
 }
 
+// The GEMV launch with its balanced grid: split tiles need a small partial
+// workspace and self-resetting counters (library scratch, zeroed once).
+// xf (fp32 activations, 16-byte aligned) selects the fused form that quantizes
+// inside the GEMV; otherwise xq/sa are the pre-quantized activations.
+int run_gemv(const char* who, int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+             const float* sa, const float* xf, int rows, int N, int K, const rt4::GemvCfg& c, hipStream_t st) {
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
+    if (sp.nrem > 0) {
+        // Sized once for the largest split any shape can need (at most one piece
+        // per CU, 4 rows), so only the first split launch on a device allocates.
+        // Under graph capture nothing may be allocated: if the workspace does not
+        // exist yet, the launch runs unsplit (same results, less balanced).
+        const size_t pb = (size_t)cus * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
+        void *part = nullptr, *cnt = nullptr;
+        if (cap != hipStreamCaptureStatusNone && !(scratch_has(kSlotGemvPart, pb) && scratch_has(kSlotGemvCnt, cb))) {
+            sp.full += sp.nrem;
+            sp.nrem = 0;
+            sp.S = 1;
+        } else {
+            if ((rc = scratch(kSlotGemvPart, pb, &part))) return rc;
+            if ((rc = scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
+            sp.part = static_cast<float*>(part);
+            sp.cnt = static_cast<int*>(cnt);
+        }
+    }
+    return hip_status(rt4::launch_gemv_w4a8(y, gsum, wq, ws, xq, sa, xf, rows, N, K, c, sp, st), who);
+}
+
+// Default launch configuration with the caller's overrides (0 keeps a default).
+int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int waves, int k_splits,
+             rt4::GemvCfg* out) {
+    rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    if (groups_per_wave > 0) {
+        c.gpw = groups_per_wave;
+        const int nc = (K / 128 + c.gpw - 1) / c.gpw;
+        c.waves = nc < rt4::kGemvMaxWaves ? nc : rt4::kGemvMaxWaves;
+    }
+    if (waves > 0) c.waves = waves;
+    if (k_splits > 0) c.max_split = k_splits;
+    if (groups_per_wave < 0 || waves < 0 || k_splits < 0 || !rt4::gemv_cfg_valid(c, K))
+        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d", who, groups_per_wave,
+                    waves, k_splits);
+    *out = c;
+    return RT4_OK;
+}
+
 int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
                    const int8_t* xq, const float* sc, int M, int N, int K, void* stream) {
     if (!c || !wq || !wsc_gm || !xq || !sc) return fail(RT4_E_ARG, "%s: null pointer", who);
@@ -152,26 +210,31 @@ int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int ro
 
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
-                        void* stream) {
+                        int k_splits, void* stream) {
     if (!y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8", rows, N, K);
     if (rc || (rc = check_gemv_align("rt4_gemv_w4a8", y, wq, ws, xq, sa))) return rc;
-    rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
-    if (groups_per_wave > 0) {
-        c.gpw = groups_per_wave;
-        const int nc = (K / 128 + c.gpw - 1) / c.gpw;
-        c.waves = nc < rt4::kGemvMaxWaves ? nc : rt4::kGemvMaxWaves;
-    }
-    if (waves > 0) c.waves = waves;
-    if (!rt4::gemv_cfg_valid(c, K))
-        return fail(RT4_E_ARG, "rt4_gemv_w4a8: bad config groups_per_wave=%d waves=%d", c.gpw, c.waves);
-    return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, xq, sa, rows, N, K, c, as_stream(stream)),
-                      "rt4_gemv_w4a8 launch");
+    rt4::GemvCfg c;
+    if ((rc = gemv_cfg("rt4_gemv_w4a8", K, rows, N, groups_per_wave, waves, k_splits, &c))) return rc;
+    return run_gemv("rt4_gemv_w4a8 launch", nullptr, y, wq, ws, xq, sa, nullptr, rows, N, K, c, as_stream(stream));
+}
+
+int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits) {
+    if (!groups_per_wave || !waves || !k_splits) return fail(RT4_E_ARG, "rt4_gemv_launch_plan: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_launch_plan", rows, N, K);
+    int cus = 0;
+    if (rc || (rc = device_cus(&cus))) return rc;
+    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    const rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
+    *groups_per_wave = c.gpw;
+    *waves = c.waves;
+    *k_splits = sp.nrem > 0 ? sp.S : 1;
+    return RT4_OK;
 }
 
 int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                     const float* sa, int rows, int N, int K, void* stream) {
-    return rt4_gemv_w4a8_q_cfg(y, wq, ws, xq, sa, rows, N, K, 0, 0, stream);
+    return rt4_gemv_w4a8_q_cfg(y, wq, ws, xq, sa, rows, N, K, 0, 0, 0, stream);
 }
 
 int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws,
@@ -181,8 +244,21 @@ int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const u
     int rc = check_gemv_shape("rt4_gemv_w4a8_groupsums", rows, N, K);
     if (rc || (rc = check_gemv_align("rt4_gemv_w4a8_groupsums", y, wq, ws, xq, sa))) return rc;
     const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
-    return hip_status(rt4::launch_gemv_w4a8(y, gsum, wq, ws, xq, sa, rows, N, K, c, as_stream(stream)),
-                      "rt4_gemv_w4a8_groupsums launch");
+    return run_gemv("rt4_gemv_w4a8_groupsums launch", gsum, y, wq, ws, xq, sa, nullptr, rows, N, K, c,
+                    as_stream(stream));
+}
+
+int rt4_gemv_w4a8_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
+                      int groups_per_wave, int waves, int k_splits, void* stream) {
+    if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_w4a8_cfg", rows, N, K);
+    if (rc) return rc;
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 16) || !aligned(ws, 2))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: misaligned pointer (wq and x need 16 bytes)");
+    rt4::GemvCfg c;
+    if ((rc = gemv_cfg("rt4_gemv_w4a8_cfg", K, rows, N, groups_per_wave, waves, k_splits, &c))) return rc;
+    return run_gemv("rt4_gemv_w4a8_cfg launch", nullptr, y, wq, ws, nullptr, nullptr, x, rows, N, K, c,
+                    as_stream(stream));
 }
 
 int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows,
@@ -192,16 +268,18 @@ int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
         return fail(RT4_E_ARG, "k_gemv_w4a8: misaligned pointer (wq needs 16 bytes)");
+    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    // Two launches, as the reference: the activation quantizer into library
+    // scratch, then the GEMV.  (The fused one-launch form, rt4_gemv_w4a8_cfg,
+    // re-quantizes the activations in every 16-row tile and measures slower.)
     void *q = nullptr, *s = nullptr;
     if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q))) return rc;
     if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s))) return rc;
     hipStream_t st = as_stream(stream);
     hipError_t e = rt4::launch_quant_act_a8(static_cast<int8_t*>(q), static_cast<float*>(s), nullptr, x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a8 quant launch");
-    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
-    return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, static_cast<const int8_t*>(q),
-                                            static_cast<const float*>(s), rows, N, K, c, st),
-                      "k_gemv_w4a8 launch");
+    return run_gemv("k_gemv_w4a8 launch", nullptr, y, wq, ws, static_cast<const int8_t*>(q),
+                    static_cast<const float*>(s), nullptr, rows, N, K, c, st);
 }
 
 int rt4_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, const float* x,

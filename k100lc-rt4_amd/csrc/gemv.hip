@@ -33,6 +33,14 @@
 //   reference's (ws*sa)*I term bit for bit (power-of-two scaling is exact); only
 //   the order of the sum over groups differs from the reference.  The W partial
 //   sums of a tile are reduced through LDS.
+// * Fused activation quantization (QIN): the whole decode linear of the
+//   reference is two launches, quant_act then the GEMV (src/k_gemv.hip:70,
+//   96-103).  Here the waves can read the fp32 activations themselves: each lane
+//   loads the 32 values of its (row, group, quarter), the four quarter lanes of a
+//   group agree on amax with two cross-row swaps, and the lane quantizes its
+//   values into the interleaved int8 operand in registers.  The dependent
+//   activation latency then hides under the weight stream instead of costing a
+//   launch of its own.  Codes and scales are bit-identical to quant_act_a8_k.
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -58,13 +66,79 @@ __device__ __forceinline__ uint4 pull_u4(uint4 v) {
     }
 }
 
-template <int M, int GPW, bool GSUM>
+// Quantize the 32 activations of one lane -- elements q*32..q*32+31 of a
+// 128-group, quarter q held by lanes j, j+16, j+32, j+48 -- as quant_act_a8_k
+// does: s = amax > 0 ? amax/127 : 1, c = clamp(rint(v/s), -128, 127).  Outputs the
+// interleaved bytes (per 8 elements [c0 c2 c4 c6 c1 c3 c5 c7]) as two dwordx4 and
+// the scale.  v/s uses a correctly rounded reciprocal y = 1/s and one
+// Markstein correction, t = RN(v*y), q = RN(t + RN(v - t*s)*y) with the residual
+// exact by FMA: for y = RN(1/s) and no underflow this is the correctly rounded
+// quotient (Markstein's theorem), i.e. bit-equal to v/s.  Scales outside
+// [2^-96, 2^100] (tiny or non-finite groups, where the residual could underflow)
+// take the IEEE division instead.
+__device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c1, (uint32_t)c0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c3, (uint32_t)c2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+__device__ __forceinline__ void quant_lane(const float4 (&x)[8], uint4& a0, uint4& a1, float& scale) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        amax = fmaxf(fmaxf(amax, fmaxf(fabsf(x[i].x), fabsf(x[i].y))), fmaxf(fabsf(x[i].z), fabsf(x[i].w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float s = amax > 0.f ? amax / 127.f : 1.f;
+    scale = s;
+    const bool fast = __all(s >= 0x1p-96f && s <= 0x1p+100f);
+    const float y = 1.f / s;
+    uint32_t d[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {  // 8 elements -> 2 dwords at a time (short live ranges)
+        const float v[8] = {x[2 * k].x, x[2 * k].y, x[2 * k].z, x[2 * k].w,
+                            x[2 * k + 1].x, x[2 * k + 1].y, x[2 * k + 1].z, x[2 * k + 1].w};
+        int c[8];
+        if (fast) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float t = v[e] * y;
+                const float r = fmaf(-t, s, v[e]);
+                c[e] = clampi((int)lrintf(fmaf(r, y, t)), -128, 127);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) c[e] = clampi((int)lrintf(v[e] / s), -128, 127);
+        }
+        d[2 * k] = pack4(c[0], c[2], c[4], c[6]);
+        d[2 * k + 1] = pack4(c[1], c[3], c[5], c[7]);
+    }
+    a0 = make_uint4(d[0], d[1], d[2], d[3]);
+    a1 = make_uint4(d[4], d[5], d[6], d[7]);
+}
+
+// Agent-coherent (sc1) 4-byte store / load of split-tile partials, each with
+// its wait in the same asm statement: the store has reached the coherent level
+// before the counter increment that publishes it, and the load's value is valid
+// before use.  (A release fence would write back the whole L2 instead.)
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0) expcnt(0)" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    float v;
+    asm volatile("global_load_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+template <int M, int GPW, bool GSUM, bool QIN>
 __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
                                                     const int8_t* __restrict__ xq,
                                                     const float* __restrict__ sa,
+                                                    const float* __restrict__ xf,
                                                     float* __restrict__ y,
-                                                    int32_t* __restrict__ gsum, int N, int K) {
+                                                    int32_t* __restrict__ gsum, int N, int K,
+                                                    GemvSplit sp) {
     constexpr int GPS = 16 / M;                  // groups per activation register set
     constexpr int NSET = (GPW + GPS - 1) / GPS;
     constexpr int NP = GPW / 2;                  // group pairs per wave
@@ -74,7 +148,14 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     const int j = lane & 15, q = lane >> 4;
     const int NG = K >> 7, RS = K >> 1;          // groups and bytes per weight row
     const int NC = (NG + GPW - 1) / GPW;         // group chunks per tile
-    const int n0 = blockIdx.x * 16;
+    // Workgroups [0, npieces) each take one K range of a remainder tile; the rest
+    // take whole tiles (see launch_gemv_w4a8).
+    const int b = blockIdx.x, npieces = sp.nrem * sp.S;
+    const bool piece = b < npieces;
+    const int rem = piece ? b / sp.S : 0, pc = piece ? b % sp.S : 0;
+    const int tile = piece ? sp.full + rem : b - npieces;
+    const int c_lo = piece ? pc * NC / sp.S : 0, c_hi = piece ? (pc + 1) * NC / sp.S : NC;
+    const int n0 = tile * 16;
     // scale slice of this wave: [16 rows][GPW/2] dwords (fp16 pairs), then the
     // reduction area; always accessed as dwords
     uint32_t* wsl = reinterpret_cast<uint32_t*>(smem) + (size_t)w * 8 * GPW;
@@ -100,7 +181,7 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
 #pragma unroll
     for (int r = 0; r < M; r++) yacc[r] = 0.f;
 
-    for (int c = w; c < NC; c += W) {
+    for (int c = c_lo + w; c < c_hi; c += W) {
         const int g0 = uniform(c * GPW);
         // (1) this wave's scales: 16 rows x GPW fp16, as dwords (even NG: every
         //     row starts 4-byte aligned) or as halves (odd NG)
@@ -120,14 +201,23 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
             sw[d] = v;
         }
         // (2) activations: set s, lane j holds row j%M of group g0 + s*GPS + j/M
+        //     (QIN: its fp32 values, quantized after the weight loads are issued)
         uint4 ax0[NSET], ax1[NSET];
+        float asc[NSET];
+        float4 xv[QIN ? NSET : 1][8];
 #pragma unroll
         for (int s = 0; s < NSET; s++) {
             int g = g0 + s * GPS + jg;
             g = g < NG ? g : NG - 1;
-            const uint4* ap = reinterpret_cast<const uint4*>(xq + (size_t)jr * K + (size_t)g * 128 + q * 32);
-            ax0[s] = ap[0];
-            ax1[s] = ap[1];
+            if constexpr (QIN) {
+                const float4* xp = reinterpret_cast<const float4*>(xf + (size_t)jr * K + (size_t)g * 128 + q * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) xv[s][i] = xp[i];
+            } else {
+                const uint4* ap = reinterpret_cast<const uint4*>(xq + (size_t)jr * K + (size_t)g * 128 + q * 32);
+                ax0[s] = ap[0];
+                ax1[s] = ap[1];
+            }
         }
         // (3) the weight stream.  A pair starting at the last group of an odd NG
         //     has no second group: its lanes read the first group again (in bounds)
@@ -145,6 +235,10 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
         for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
             const int dw = q + 4 * d;
             if (dw < GPW / 2) wsl[j * (GPW / 2) + dw] = sw[d];
+        }
+        if constexpr (QIN) {
+#pragma unroll
+            for (int s = 0; s < NSET; s++) quant_lane(xv[s], ax0[s], ax1[s], asc[s]);
         }
 
 #pragma unroll
@@ -193,13 +287,20 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
                     const uint32_t pair = wsl[j * (GPW / 2) + p];
                     const float s16 = f16_bits_to_f32((uint16_t)(h ? pair >> 16 : pair & 0xFFFFu)) * 0.0625f;
 #pragma unroll
-                    for (int r = 0; r < M; r++) yacc[r] = fmaf((float)acc[r], s16 * sa[(size_t)r * NG + g], yacc[r]);
+                    for (int r = 0; r < M; r++) {
+                        float a_s;
+                        if constexpr (QIN)  // the scale of (row r, group g) sits in lane (u % GPS) * M + r
+                            a_s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(asc[u / GPS]), (u % GPS) * M + r));
+                        else
+                            a_s = sa[(size_t)r * NG + g];
+                        yacc[r] = fmaf((float)acc[r], s16 * a_s, yacc[r]);
+                    }
                 }
             }
         }
     }
 
-    if (W == 1) {
+    if (W == 1 && !piece) {
         if (lane < 16 && n0 + lane < N)
 #pragma unroll
             for (int r = 0; r < M; r++) y[(size_t)r * N + n0 + lane] = yacc[r];
@@ -209,33 +310,67 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
 #pragma unroll
         for (int r = 0; r < M; r++) red[(w * M + r) * 16 + lane] = yacc[r];
     __syncthreads();
-    if (threadIdx.x < M * 16) {
-        const int cl = threadIdx.x & 15, r = threadIdx.x >> 4;
-        float s = 0.f;
-        for (int v = 0; v < W; v++) s += red[(v * M + r) * 16 + cl];
-        if (n0 + cl < N) y[(size_t)r * N + n0 + cl] = s;
+    const int cl = threadIdx.x & 15, rr = threadIdx.x >> 4;
+    float tot = 0.f;
+    if (threadIdx.x < M * 16)
+        for (int v = 0; v < W; v++) tot += red[(v * M + rr) * 16 + cl];
+    if (!piece) {
+        if (threadIdx.x < M * 16 && n0 + cl < N) y[(size_t)rr * N + n0 + cl] = tot;
+        return;
     }
+    // A K range of a split tile: publish the partial (agent-coherent store), count
+    // the pieces in, and let the last one sum all pieces in order (deterministic)
+    // and reset the counter for the next call.  No workgroup waits for another.
+    __shared__ int s_last;
+    if (threadIdx.x < M * 16) store_dev(sp.part + ((size_t)b * M + rr) * 16 + cl, tot);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(sp.cnt + rem, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sp.S - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x < M * 16) {
+        float sum = 0.f;
+        for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + ((size_t)(rem * sp.S + v) * M + rr) * 16 + cl);
+        if (n0 + cl < N) y[(size_t)rr * N + n0 + cl] = sum;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + rem, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int M, int GPW, bool GSUM>
+template <int M, int GPW, bool GSUM, bool QIN>
 hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
-                      const float* sa, int N, int K, int waves, hipStream_t st) {
+                      const float* sa, const float* xf, int N, int K, int waves, const GemvSplit& sp,
+                      hipStream_t st) {
     const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * M * 16 * sizeof(float);
-    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, GSUM>), dim3((N + 15) / 16), dim3(64 * waves), smem, st, wq, ws,
-                       xq, sa, y, gsum, N, K);
+    const int grid = sp.full + sp.nrem * sp.S;
+    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, GSUM, QIN>), dim3(grid), dim3(64 * waves), smem, st, wq, ws, xq, sa,
+                       xf, y, gsum, N, K, sp);
     return hipGetLastError();
 }
 
-template <int M, bool GSUM>
+template <int M, bool GSUM, bool QIN>
 hipError_t launch_m(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
-                    const float* sa, int N, int K, const GemvCfg& c, hipStream_t st) {
+                    const float* sa, const float* xf, int N, int K, const GemvCfg& c, const GemvSplit& sp,
+                    hipStream_t st) {
     switch (c.gpw) {
-        case 2: return launch_one<M, 2, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
-        case 4: return launch_one<M, 4, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
-        case 6: return launch_one<M, 6, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
-        case 8: return launch_one<M, 8, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
-        case 10: return launch_one<M, 10, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
-        case 12: return launch_one<M, 12, GSUM>(y, gsum, wq, ws, xq, sa, N, K, c.waves, st);
+        case 2: return launch_one<M, 2, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 4: return launch_one<M, 4, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 6: return launch_one<M, 6, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 8: return launch_one<M, 8, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 10: return launch_one<M, 10, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 12: return launch_one<M, 12, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <bool GSUM, bool QIN>
+hipError_t launch_rows(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                       const float* sa, const float* xf, int rows, int N, int K, const GemvCfg& c,
+                       const GemvSplit& sp, hipStream_t st) {
+    switch (rows) {
+        case 1: return launch_m<1, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st);
+        case 2: return launch_m<2, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st);
+        case 3: return launch_m<3, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st);
+        case 4: return launch_m<4, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st);
     }
     return hipErrorInvalidValue;
 }
@@ -243,18 +378,23 @@ hipError_t launch_m(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t*
 }  // namespace
 
 GemvCfg gemv_default_cfg(int rows, int N, int K) {
-    (void)rows;
     (void)N;
     const int NG = K / kGroup;
     GemvCfg c;
-    // measured on MI355X: ~10 groups per wave for the 27B shapes (K = 5120: 4
-    // waves per tile; K = 17408: 12 groups -> 12 waves); at most 16 waves, larger
-    // K loops over group chunks inside each wave.
-    c.gpw = NG >= 120 ? 12 : 10;
+    // Measured on MI355X over the 27B shapes (K = 5120 and 17408, N = 5120 and
+    // 17408).  One activation row: 10 groups per wave at K = 5120 (4 waves),
+    // 6 at K = 17408; two rows: 8; three or four rows (3-4x the activation
+    // registers): 4.  Waves: every chunk of the tile at once up to 8, then about
+    // a third of the chunks (each wave loops), at most 16.
+    c.gpw = rows == 1 ? (NG <= 64 ? 10 : 6) : rows == 2 ? 8 : 4;
     const int ng_even = (NG + 1) & ~1;
     if (c.gpw > ng_even) c.gpw = ng_even;
-    int nc = (NG + c.gpw - 1) / c.gpw;
-    c.waves = nc < kGemvMaxWaves ? nc : kGemvMaxWaves;
+    const int nc = (NG + c.gpw - 1) / c.gpw;
+    int w = (nc + 2) / 3;
+    w = w > 8 ? w : 8;
+    w = w < nc ? w : nc;
+    c.waves = w < kGemvMaxWaves ? w : kGemvMaxWaves;
+    c.max_split = 0;
     return c;
 }
 
@@ -262,28 +402,49 @@ bool gemv_cfg_valid(const GemvCfg& c, int K) {
     const int NG = K / kGroup;
     if (c.gpw < 2 || c.gpw > 12 || (c.gpw & 1)) return false;
     const int nc = (NG + c.gpw - 1) / c.gpw;
-    return c.waves >= 1 && c.waves <= kGemvMaxWaves && c.waves <= nc;
+    return c.waves >= 1 && c.waves <= kGemvMaxWaves && c.waves <= nc && c.max_split >= 0 && c.max_split <= 64;
+}
+
+GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus) {
+    // Whole 16-row tiles in a multiple of the CU count; the remaining tiles are
+    // cut along K into S pieces, about one piece per CU, so every CU streams the
+    // same number of weight bytes (a round of whole tiles with a few tiles left
+    // over would otherwise run at a fraction of the machine).  The combine costs a
+    // round trip through L2, which only pays for deep K: by default a piece keeps
+    // at least 32 groups (K = 17408 gains ~25%, K = 5120 loses ~5% when split).
+    GemvSplit sp{};
+    const int ntiles = (N + 15) / 16;
+    const int NC = (K / kGroup + c.gpw - 1) / c.gpw;
+    cus = cus > 0 ? cus : 256;
+    sp.full = ntiles / cus * cus;
+    sp.nrem = ntiles - sp.full;
+    sp.S = 1;
+    if (sp.nrem > 0) {
+        int S = cus / sp.nrem;
+        S = S < NC ? S : NC;
+        const int cap = c.max_split > 0 ? c.max_split : (K / kGroup) / 32;
+        S = S < cap ? S : cap;
+        sp.S = S > 1 ? S : 1;
+    }
+    if (sp.S == 1) {            // nothing to split: all tiles whole
+        sp.full = ntiles;
+        sp.nrem = 0;
+    }
+    return sp;
+}
+
+size_t gemv_part_bytes(const GemvSplit& sp, int rows) {
+    return (size_t)sp.nrem * sp.S * rows * 16 * sizeof(float);
 }
 
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,
-                            const int8_t* xq, const float* sa, int rows, int N, int K,
-                            const GemvCfg& cfg, hipStream_t st) {
-    if (gsum) {
-        switch (rows) {
-            case 1: return launch_m<1, true>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 2: return launch_m<2, true>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 3: return launch_m<3, true>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 4: return launch_m<4, true>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-        }
-    } else {
-        switch (rows) {
-            case 1: return launch_m<1, false>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 2: return launch_m<2, false>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 3: return launch_m<3, false>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-            case 4: return launch_m<4, false>(y, gsum, wq, ws, xq, sa, N, K, cfg, st);
-        }
-    }
-    return hipErrorInvalidValue;
+                            const int8_t* xq, const float* sa, const float* xf, int rows, int N, int K,
+                            const GemvCfg& cfg, const GemvSplit& sp, hipStream_t st) {
+    if (xf)  // the exact group sums are a test hook of the pre-quantized form only
+        return gsum ? hipErrorInvalidValue
+                    : launch_rows<false, true>(y, gsum, wq, ws, xq, sa, xf, rows, N, K, cfg, sp, st);
+    return gsum ? launch_rows<true, false>(y, gsum, wq, ws, xq, sa, xf, rows, N, K, cfg, sp, st)
+                : launch_rows<false, false>(y, gsum, wq, ws, xq, sa, xf, rows, N, K, cfg, sp, st);
 }
 
 }  // namespace rt4

@@ -24,13 +24,27 @@ hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG
 struct GemvCfg {
     int gpw;    // K groups per wave (even, 2..12)
     int waves;  // waves per workgroup; they share one 16-row tile and split its K groups
+    int max_split;  // leftover tiles are cut along K into at most this many pieces (1: never,
+                    // 0: as many as keep 32 groups per piece)
 };
 constexpr int kGemvMaxWaves = 16;
 GemvCfg gemv_default_cfg(int rows, int N, int K);
 bool gemv_cfg_valid(const GemvCfg& c, int K);
+// Grid of the GEMV: `full` whole 16-row tiles, then `nrem` tiles cut along K into
+// S pieces each, whose partials (part: nrem*S*rows*16 floats) are summed by the
+// last piece to arrive (cnt: nrem counters, zero between calls).
+struct GemvSplit {
+    int full, nrem, S;
+    float* part;
+    int* cnt;
+};
+GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus);
+size_t gemv_part_bytes(const GemvSplit& sp, int rows);
+// Activations either pre-quantized (xq, sa; xf null) or fp32 xf [rows][K], 16-byte
+// aligned, quantized inside the kernel exactly as launch_quant_act_a8 would.
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,
-                            const int8_t* xq, const float* sa, int rows, int N, int K,
-                            const GemvCfg& cfg, hipStream_t st);
+                            const int8_t* xq, const float* sa, const float* xf, int rows, int N, int K,
+                            const GemvCfg& cfg, const GemvSplit& sp, hipStream_t st);
 
 // ---- prefill GEMM (gemm.hip)
 // C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],

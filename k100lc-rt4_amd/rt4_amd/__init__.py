@@ -28,8 +28,9 @@ GROUP = 128
 # Every symbol include/rt4k.h declares (checked by the CPU test suite).
 C_EXPORTS = (
     "rt4_last_error", "rt4_abi_version",
-    "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_w4a8_groupsums",
-    "rt4_gemv_w4a8", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
+    "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
+    "rt4_gemv_w4a8_groupsums",
+    "rt4_gemv_w4a8", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
     "rt4_make_group_major", "rt4_quant_rows_a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
     "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
@@ -58,9 +59,11 @@ _I = ctypes.c_int
 _SIGS = {
     "rt4_quant_act_a8": [_P, _P, _P, _P, _I, _I, _P],
     "rt4_gemv_w4a8_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
-    "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_gemv_launch_plan": [_I, _I, _I, _P, _P, _P],
     "rt4_gemv_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_cfg": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_a8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_i8": [_P, _P, _P, _I, _I, _I, _I, _P],
     "rt4_digits_to_i8": [_P, _P, _P, _I, _I, _P],
@@ -149,15 +152,25 @@ def quant_act_a8(x, want_sums: bool = False):
     return (xq, sa, asu) if want_sums else (xq, sa)
 
 
-def gemv_w4a8_q(wq, ws, xq, sa, out=None, groups_per_wave: int = 0, waves: int = 0):
-    """W4A8 GEMV on quantized activations.  wq int32/uint32 [N, K/8], ws int16/fp16 [N, K/128]."""
+def gemv_w4a8_q(wq, ws, xq, sa, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0):
+    """W4A8 GEMV on quantized activations.  wq int32/uint32 [N, K/8], ws int16/fp16 [N, K/128].
+
+    groups_per_wave / waves / k_splits override the launch configuration (0 keeps
+    the default; k_splits=1 keeps every 16-row tile whole)."""
     torch = _torch()
     rows, K = xq.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, xq.device)
     _check(lib().rt4_gemv_w4a8_q_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(xq), _ptr(sa), rows, N, K,
-                                     groups_per_wave, waves, _stream()))
+                                     groups_per_wave, waves, k_splits, _stream()))
     return y
+
+
+def gemv_launch_plan(rows: int, N: int, K: int) -> dict:
+    """The default GEMV launch configuration for this shape on the current device."""
+    g, w, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(lib().rt4_gemv_launch_plan(rows, N, K, ctypes.byref(g), ctypes.byref(w), ctypes.byref(s)))
+    return {"groups_per_wave": g.value, "waves": w.value, "k_splits": s.value}
 
 
 def gemv_w4a8_groupsums(wq, ws, xq, sa):
@@ -172,13 +185,21 @@ def gemv_w4a8_groupsums(wq, ws, xq, sa):
     return y, gs
 
 
-def gemv_w4a8(wq, ws, x, out=None):
-    """Drop-in k_gemv_w4a8: quantize x f32 [rows, K] and multiply (rows <= 4)."""
+def gemv_w4a8(wq, ws, x, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0):
+    """Drop-in k_gemv_w4a8: quantize x f32 [rows, K] and multiply (rows <= 4).
+
+    Two launches (quantizer, GEMV).  A launch configuration (see gemv_w4a8_q)
+    selects rt4_gemv_w4a8_cfg instead: one launch that quantizes inside the GEMV
+    (x 16-byte aligned), bit-identical output."""
     torch = _torch()
     rows, K = x.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, x.device)
-    _check(lib().rt4_gemv_w4a8(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, _stream()))
+    if groups_per_wave or waves or k_splits:
+        _check(lib().rt4_gemv_w4a8_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, groups_per_wave, waves,
+                                       k_splits, _stream()))
+    else:
+        _check(lib().rt4_gemv_w4a8(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, _stream()))
     return y
 
 

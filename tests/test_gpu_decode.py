@@ -89,6 +89,84 @@ def test_gemv_every_config(rt4, orc, torch_gpu, gpw, waves):
     assert rel_l2(host(y), ref) < TIGHT
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(4, 300, 3072, 8), (1, 300, 3072, 64), (4, 4176, 8192, 1),
+                                           (4, 4176, 8192, 2), (2, 4176, 8192, 5), (3, 4176, 8192, 64),
+                                           (4, 4176, 8192, 0), (1, 4100, 17408, 0)])
+def test_gemv_k_split(rt4, orc, torch_gpu, M, N, K, splits):
+    """Leftover tiles cut along K (pieces combined by the last to finish) against
+    whole tiles and the oracle; the combine only changes the fp32 sum order."""
+    print(f"case gemv_split M={M} N={N} K={K} k_splits={splits}", flush=True)
+    c, wq, ws, x = _gemv_inputs(torch_gpu, 9, M, N, K)
+    xq, sa = rt4.quant_act_a8(x)
+    y = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=splits)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=splits)    # counters were left at zero
+    torch_gpu.cuda.synchronize()
+    ref = orc.gemv_w4a8(c["wq"], c["ws"], c["x"])
+    assert rel_l2(host(y), ref) < TIGHT
+    assert np.array_equal(host(y), host(y2))
+
+
+def fused_edge_acts(rng, M, K):
+    """edge_acts plus groups that take every branch of the in-GEMV quantizer: all
+    zero (s = 1), tiny and huge magnitudes (scale outside [2^-96, 2^100]: IEEE
+    division), exact rounding ties v/s = k + 1/2 (power-of-two scale), denormals."""
+    x = edge_acts(rng, M, K)
+    NG = K // 128
+    for r in range(M):
+        g = (3 * r) % NG
+        x[r, g * 128:(g + 1) * 128] = rng.standard_normal(128).astype(np.float32) * np.float32(1e-33)
+        g = (3 * r + 1) % NG
+        x[r, g * 128:(g + 1) * 128] = rng.standard_normal(128).astype(np.float32) * np.float32(1e33)
+        g = (3 * r + 2) % NG
+        e = float(rng.integers(-20, 20))
+        k = rng.integers(-127, 127, 128).astype(np.float32)
+        x[r, g * 128:(g + 1) * 128] = np.ldexp(k + np.float32(0.5), int(e)).astype(np.float32)
+        x[r, g * 128] = np.float32(np.ldexp(127.0, int(e)))          # amax: s = 2^e exactly
+    if NG > 4:
+        x[0, 4 * 128:4 * 128 + 64] = np.float32(1e-40)                # denormal inputs
+    return x
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [(1, 5120, 5120, None), (2, 1000, 5120, None), (3, 2064, 17408, None),
+                                       (4, 17408, 5120, None), (4, 5120, 17408, None), (4, 300, 3072, (2, 12, 1)),
+                                       (4, 300, 3072, (6, 4, 3)), (1, 520, 2944, (10, 2, 0)), (2, 64, 40960, (8, 16, 8)),
+                                       (3, 96, 1920, (12, 1, 1))])
+def test_gemv_fused_quant_equals_two_launches(rt4, orc, torch_gpu, M, N, K, cfg):
+    """The one-launch linear (activations quantized in the GEMV's registers) against
+    rt4_quant_act_a8 + the GEMV on the same config: outputs identical bit for bit
+    (same codes, scales and sum order), and within the bar of the oracle."""
+    print(f"case gemv_fused M={M} N={N} K={K} cfg={cfg}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K)
+    c = workload.gemv_case(N=N, K=K, M=M, seed=int(rng.integers(1 << 30)))
+    x_np = fused_edge_acts(rng, M, K)
+    wq, ws, x = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["ws"]), dev(torch_gpu, x_np)
+    g, w, s = cfg or (0, 0, 0)
+    y = rt4.gemv_w4a8(wq, ws, x, groups_per_wave=g, waves=w, k_splits=s)
+    xq, sa = rt4.quant_act_a8(x)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=g, waves=w, k_splits=s)
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
+    if N * K <= 5120 * 5120:
+        ref = orc.gemv_w4a8(c["wq"], c["ws"], x_np)
+        assert rel_l2(host(y), ref) < TIGHT
+
+
+def test_gemv_unaligned_activations(rt4, orc, torch_gpu):
+    """x not 16-byte aligned: the drop-in quantizes separately; the fused config
+    entry refuses it."""
+    M, N, K = 2, 256, 1024
+    print(f"case gemv_unaligned M={M} N={N} K={K}", flush=True)
+    c, wq, ws, _ = _gemv_inputs(torch_gpu, 11, M, N, K)
+    buf = torch_gpu.zeros(M * K + 1, dtype=torch_gpu.float32, device="cuda")
+    x = buf[1:].view(M, K)
+    x.copy_(torch_gpu.from_numpy(c["x"]).cuda())
+    y = rt4.gemv_w4a8(wq, ws, x)
+    torch_gpu.cuda.synchronize()
+    assert rel_l2(host(y), orc.gemv_w4a8(c["wq"], c["ws"], c["x"])) < TIGHT
+    with pytest.raises(rt4.RT4Error, match="misaligned"):
+        rt4.gemv_w4a8(wq, ws, x, groups_per_wave=4)
+
+
 @pytest.mark.parametrize("name", ["c0", "c1_gate_up", "c1_down"])
 def test_gemv_benchmark_shapes(rt4, orc, torch_gpu, name):
     M, N, K = workload.GEMV_SHAPES[name]
