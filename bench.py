@@ -192,6 +192,50 @@ def gemm_table(torch, rt4_amd, workload, gen) -> dict:
     return out
 
 
+def attn_table(torch, rt4_amd, workload, gen) -> dict:
+    """int4-KV FlashAttention prefill: 24 query heads over 4 KV
+    heads, head dim 256, 1024 new queries over a 32768-token cache, causal.  Effective
+    int8-MFMA TOPS counts the two contractions over the keys each query sees
+    (2 * 2 * D per visible (query, key) pair per head); plus the Q quantizer and the
+    K/V cache append of the 1024 new tokens."""
+    c4 = workload.ATTN_C4
+    n_q, ctx, H, KVH, D = c4["n_q"], c4["ctx"], c4["H"], c4["KVH"], c4["D"]
+    n_kv = ctx + n_q
+    q, k, v = workload.attn_torch(n_q, n_kv, H, KVH, D, generator=gen)
+    qq, qs = rt4_amd.attn_q_quant(q, n_q)
+    kc = torch.zeros((KVH, n_kv, D // 8), dtype=torch.int32, device="cuda")
+    ksc = torch.ones((KVH, 2, n_kv), device="cuda")
+    vc = torch.zeros((KVH, n_kv // 8, D), dtype=torch.int32, device="cuda")
+    vsc = torch.ones((KVH, n_kv // 64, D), device="cuda")
+    stage = torch.zeros((KVH, 64, D), device="cuda")
+    rt4_amd.kv_append_k(kc, ksc, k, 0)
+    rt4_amd.kv_append_v(vc, vsc, stage, v, 0)
+    out = rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH)
+    torch.cuda.synchronize()
+    reps = 3
+
+    def fa():
+        for _ in range(reps):
+            rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH, out=out)
+
+    us = timed_graph(torch, fa) * 1e3 / reps
+    ops = sum(ctx + i + 1 for i in range(n_q)) * 2 * 2 * D * H
+    k_new, v_new = k[ctx:].contiguous(), v[ctx:].contiguous()
+
+    def feed():
+        rt4_amd.attn_q_quant(q, n_q, qq=qq, qs=qs)
+        rt4_amd.kv_append_k(kc, ksc, k_new, ctx)
+        rt4_amd.kv_append_v(vc, vsc, stage, v_new, ctx)
+
+    feed_us = timed_graph(torch, feed) * 1e3
+    res = {"attn_c4_prefill": {"us": round(us, 1), "TOPS_effective": round(ops / us / 1e6, 1),
+                               "frac_i8_peak": round(ops / us / 1e6 / I8_PEAK_TOPS, 4),
+                               "feeders_us": round(feed_us, 2)}}
+    del q, k, v, qq, qs, kc, ksc, vc, vsc, stage, out, k_new, v_new
+    torch.cuda.empty_cache()
+    return res
+
+
 def load_traffic(key: str):
     """Bytes per launch of `key` measured by the FETCH_SIZE / WRITE_SIZE counter runs
     (rt4_amd.profiling), or None when that summary is absent."""
@@ -369,6 +413,7 @@ def main() -> int:
         del layers, gu_mats, d_mats, c0_mats
         torch.cuda.empty_cache()
         kernels.update(gemm_table(torch, rt4_amd, workload, gen))
+        kernels.update(attn_table(torch, rt4_amd, workload, gen))
         lm = [workload.weights_torch(248320, 5120, generator=gen) for _ in range(2)]
         y_lm = torch.empty((M, 248320), device="cuda")
 

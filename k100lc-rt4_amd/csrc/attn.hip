@@ -128,37 +128,65 @@ __global__ __launch_bounds__(256) void kv_append_k_k(uint32_t* __restrict__ kc, 
     if (e8 % GL == 0) ksc[((size_t)h * ng + e8 / GL) * kv_total + kv] = s;
 }
 
-// V cache append (restates kv_append_v_k, src/k_new.hip:351-392).  One thread per
-// (head, dim) walks the tiles the append touches: new values go into the fp32
-// stage [H][BG][D] (the current partial tile), the tile is re-quantized from its
-// valid slots, slots past the last valid one get code 0.  grid (H, D/64), 64 threads.
+// V cache append (restates kv_append_v_k, src/k_new.hip:351-392).  The reference
+// walks the 64-key tiles an append touches with one thread per (head, dim): new
+// values go into the fp32 stage [H][BG][D] (the current partial tile), each tile
+// is re-quantized from its valid slots (scale amax/7 per (tile, dim)), slots past
+// the last valid one get code 0.  Every tile but the first of an append depends
+// only on the new values, so here the tiles run in parallel (phase 1: one
+// workgroup per (head, 64 dims, tile)), the first tile reading the stage's
+// earlier slots; phase 2 then leaves the stage exactly as the sequential walk
+// would (the last tile's values, and beneath them those of the tile before it).
+// Phase 1 writes no stage slot, so the two phases are ordered by the stream.
 __global__ __launch_bounds__(64) void kv_append_v_k(uint32_t* __restrict__ vc, float* __restrict__ vsc,
-                                                    float* __restrict__ stage, const float* __restrict__ vf,
+                                                    const float* __restrict__ stage, const float* __restrict__ vf,
                                                     int t0, int T, int H, int D, int BG, int kv_total) {
+    const int h = blockIdx.x, d = blockIdx.y * 64 + threadIdx.x, ti = blockIdx.z;
+    if (d >= D) return;
+    const int first = t0 / BG, tile = first + ti, slot0 = ti == 0 ? t0 % BG : 0;
+    const int done = ti == 0 ? 0 : (BG - t0 % BG) + (ti - 1) * BG;  // new values before this tile
+    const int n = (T - done < BG - slot0) ? (T - done) : (BG - slot0);
+    const int nval = slot0 + n;
+    const float* st = stage + (size_t)h * BG * D + d;
+    const float* src = vf + ((size_t)(done - slot0) * H + h) * D + d;  // slot i >= slot0 -> src[i*H*D]
+    float amax = 0.f;
+    for (int i = 0; i < nval; i++) {
+        const float v = i < slot0 ? st[(size_t)i * D] : src[(size_t)i * H * D];
+        amax = fmaxf(amax, fabsf(v));
+    }
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
+    uint32_t* out = vc + ((size_t)h * (kv_total / 8) + (size_t)tile * (BG / 8)) * D + d;
+    for (int i = 0; i < BG; i += 8) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int k = i + e;
+            const float v = k < nval ? (k < slot0 ? st[(size_t)k * D] : src[(size_t)k * H * D]) : 0.f;
+            w |= code4(v, s) << (4 * e);
+        }
+        out[(size_t)(i / 8) * D] = w;
+    }
+}
+
+// Phase 2: the stage after the append.  Slot k holds the value of the last tile
+// this append wrote it in: the last tile for its slots [slot0, nval), the tile
+// before it (when this append also wrote that one) for the slots above nval,
+// earlier content otherwise.  grid (H, D/64), 64 threads.
+__global__ __launch_bounds__(64) void kv_stage_v_k(float* __restrict__ stage, const float* __restrict__ vf, int t0,
+                                                   int T, int H, int D, int BG) {
     const int h = blockIdx.x, d = blockIdx.y * 64 + threadIdx.x;
     if (d >= D) return;
+    const int first = t0 / BG, last = (t0 + T - 1) / BG;
+    const int nval = (t0 + T - 1) % BG + 1;
+    const int lo_last = last == first ? t0 % BG : 0;
+    const int lo_prev = last - 1 == first ? t0 % BG : 0;
     float* st = stage + (size_t)h * BG * D + d;
-    uint32_t* out = vc + (size_t)h * (kv_total / 8) * D;
-    int done = 0;
-    while (done < T) {
-        const int kv = t0 + done, tile = kv / BG, slot0 = kv % BG;
-        const int n = (T - done < BG - slot0) ? (T - done) : (BG - slot0);
-        for (int i = 0; i < n; i++) st[(size_t)(slot0 + i) * D] = vf[((size_t)(done + i) * H + h) * D + d];
-        const int nval = slot0 + n;
-        float amax = 0.f;
-        for (int i = 0; i < nval; i++) amax = fmaxf(amax, fabsf(st[(size_t)i * D]));
-        const float s = amax > 0.f ? amax / 7.f : 1.f;
-        vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
-        for (int i = 0; i < BG; i += 8) {
-            uint32_t w = 0;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = (i + e < nval) ? st[(size_t)(i + e) * D] : 0.f;
-                w |= code4(v, s) << (4 * e);
-            }
-            out[((size_t)tile * (BG / 8) + i / 8) * D + d] = w;
-        }
-        done += n;
+    for (int k = 0; k < BG; k++) {
+        int tok = -1;  // index of the new value that ends up in slot k
+        if (k >= lo_last && k < nval) tok = last * BG + k - t0;
+        else if (k >= nval && last > first && k >= lo_prev) tok = (last - 1) * BG + k - t0;
+        if (tok >= 0) st[(size_t)k * D] = vf[((size_t)tok * H + h) * D + d];
     }
 }
 
@@ -471,8 +499,12 @@ hipError_t launch_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0,
 hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
                               int D, int BG, int kv_total, hipStream_t st) {
     if (T <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_append_v_k, dim3(H, (D + 63) / 64), dim3(64), 0, st, vc, vsc, stage, vf, t0, T, H, D, BG,
-                       kv_total);
+    const int ntile = (t0 + T - 1) / BG - t0 / BG + 1;
+    hipLaunchKernelGGL(kv_append_v_k, dim3(H, (D + 63) / 64, ntile), dim3(64), 0, st, vc, vsc, stage, vf, t0, T, H,
+                       D, BG, kv_total);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kv_stage_v_k, dim3(H, (D + 63) / 64), dim3(64), 0, st, stage, vf, t0, T, H, D, BG);
     return hipGetLastError();
 }
 

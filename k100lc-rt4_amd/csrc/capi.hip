@@ -395,7 +395,8 @@ int rt4_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0, int T, in
 int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D,
                     int BG, int kv_total, void* stream) {
     if (!vc || !vsc || !stage || !vf) return fail(RT4_E_ARG, "k_kv_append_v: null pointer");
-    if (t0 < 0 || T < 0 || H < 1 || D <= 0 || BG <= 0 || BG % 8 || kv_total % BG || (long long)t0 + T > kv_total)
+    if (t0 < 0 || T < 0 || H < 1 || D <= 0 || BG <= 0 || BG % 8 || kv_total % BG || (long long)t0 + T > kv_total ||
+        (T > 0 && (t0 + T - 1) / BG - t0 / BG + 1 > 65535) || (D + 63) / 64 > 65535)
         return fail(RT4_E_SHAPE, "k_kv_append_v: t0=%d T=%d H=%d D=%d BG=%d kv_total=%d", t0, T, H, D, BG,
                     kv_total);
     return hip_status(rt4::launch_kv_append_v(vc, vsc, stage, vf, t0, T, H, D, BG, kv_total, as_stream(stream)),
