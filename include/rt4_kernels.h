@@ -45,8 +45,11 @@ void k_kv_append_k(u32* kc, float* ksc, const float* kf, int t0, int T, int H, i
 void k_kv_append_v(u32* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H, int D,
                    int BG, int kv_total);
 
-// src/kernels.h:81 -- int4-KV causal attention.  The prefill kernel serves both
-// of the reference's branches (see shim.cpp); pout/pmax/psum/max_split are unused.
+// src/kernels.h:81 -- int4-KV causal attention.  The prefill branch runs this
+// library's kernel; the single-row decode branch (n_row == 1, off + 1 == n_kv)
+// calls the caller's own k_attention_decode (src/k_fa.hip:244-259) when the
+// executable defines it, else the prefill kernel (the reference's RT_ATTN_OLD=1
+// path).  pout/pmax/psum/max_split are the decode routine's split-KV scratch.
 void k_attention(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc,
                  const u32* vc, const float* vsc, int n_q, int n_row, int n_kv, int off, int n_tile,
                  int n_heads, int ratio, int kv_cap, float* pout, float* pmax, float* psum,

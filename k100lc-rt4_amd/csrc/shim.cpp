@@ -58,18 +58,24 @@ void k_kv_append_v(u32* vc, float* vsc, float* stage, const float* vf, int t0, i
     if (rt4_kv_append_v(vc, vsc, stage, vf, t0, T, H, D, BG, kv_total, nullptr) != RT4_OK) die("k_kv_append_v");
 }
 
-// src/k_fa.hip:282-300.  Both branches run the prefill kernel here: the
-// reference's single-row decode kernel (fa_decode_k, fp32 P with split-KV) is
-// not rebuilt, so a decode call (n_row == 1, off + 1 == n_kv) takes the path
-// the reference takes under RT_ATTN_OLD=1; the split-KV scratch is unused.
+// The reference's single-row decode attention (src/k_fa.hip:244-259: fa_decode_k,
+// fp32 P, split-KV) is not rebuilt.  When the executable still defines it (the
+// rest of src/k_fa.hip stays in the link), the decode branch calls it, as the
+// reference dispatcher does; otherwise the decode branch runs the prefill
+// kernel, which is the path the reference takes under RT_ATTN_OLD=1.
+void k_attention_decode(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc,
+                        const u32* vc, const float* vsc, int n_kv, int kv_cap, int n_heads, int ratio, int n_q,
+                        float* pout, float* pmax, float* psum, int max_split) __attribute__((weak));
+
+// src/k_fa.hip:282-300
 void k_attention(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc, const u32* vc,
                  const float* vsc, int n_q, int n_row, int n_kv, int off, int n_tile, int n_heads, int ratio,
                  int kv_cap, float* pout, float* pmax, float* psum, int max_split) {
-    (void)n_row;
-    (void)pout;
-    (void)pmax;
-    (void)psum;
-    (void)max_split;
+    if (n_row == 1 && off + 1 == n_kv && k_attention_decode) {
+        k_attention_decode(out, qq, qsc, kc, ksc, vc, vsc, n_kv, kv_cap, n_heads, ratio, n_q, pout, pmax, psum,
+                           max_split);
+        return;
+    }
     if (rt4_attention_prefill(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap,
                               nullptr) != RT4_OK)
         die("k_attention");

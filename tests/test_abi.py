@@ -91,6 +91,22 @@ def test_shim_exits_like_the_reference():
     assert "k_gemv_w4a8" in r.stdout and "rows=5" in r.stdout
 
 
+def test_shim_attention_decode_branch_uses_callers_decode_kernel():
+    """k_attention hands the single-row decode branch to the executable's own
+    k_attention_decode (src/k_fa.hip:282-292) with the reference's arguments."""
+    src = ROOT / "tests" / "shim_decode_caller.cpp"
+    exe = ROOT / "tests" / "_shim_decode_caller"
+    lib = ROOT / "k100lc-rt4_amd" / "rt4_amd" / "lib"
+    subprocess.run(["g++", "-std=c++17", "-I", str(ROOT / "include"), str(src), "-L", str(lib),
+                    "-lrt4k", f"-Wl,-rpath,{lib}", "-o", str(exe)], check=True)
+    try:
+        r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    finally:
+        exe.unlink(missing_ok=True)
+    assert r.returncode == 7, (r.returncode, r.stdout, r.stderr)
+    assert "decode n_kv=300 kv_cap=4096 n_heads=24 ratio=6 n_q=64 max_split=8" in r.stdout
+
+
 def test_single_hip_runtime_in_process(rt4):
     """librt4k.so binds to the HIP runtime torch already loaded (one runtime per process)."""
     import torch  # noqa: F401
