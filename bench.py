@@ -169,6 +169,11 @@ def gemm_table(torch, rt4_amd, workload, gen) -> dict:
         c = torch.empty((M, N), device="cuda")
         c2 = torch.empty((M, N), device="cuda")
         reps = 10
+        aq4, sc4 = rt4_amd.quant_rows_a4(x)
+
+        def gemm4():
+            for _ in range(reps):
+                rt4_amd.gemm_w4a4(wq, sb, aq4, sc4, out=c)
 
         def gemm():
             for _ in range(reps):
@@ -180,14 +185,16 @@ def gemm_table(torch, rt4_amd, workload, gen) -> dict:
 
         rt4_amd.gemm_w4a8_i8(wq, sb, xq, sc, out=c)           # eager first calls: kernel attributes
         rt4_amd.gemm_w4a8(wq, sb, qh, ql, sc_, sc16, out=c, c2=c2)
+        rt4_amd.gemm_w4a4(wq, sb, aq4, sc4, out=c)
         torch.cuda.synchronize()
         us = timed_graph(torch, gemm) * 1e3 / reps
         us_d = timed_graph(torch, dropin) * 1e3 / reps
+        us_4 = timed_graph(torch, gemm4) * 1e3 / reps
         ops = 2 * M * N * K
         out[f"gemm_{name}"] = {"us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
                                "frac_i8_peak": round(ops / us / 1e6 / I8_PEAK_TOPS, 4),
-                               "dropin_us": round(us_d, 2)}
-        del wq, ws, sb, x, xq, sc, qh, ql, sc_, sc16, c, c2
+                               "dropin_us": round(us_d, 2), "w4a4_dropin_us": round(us_4, 2)}
+        del wq, ws, sb, x, xq, sc, qh, ql, sc_, sc16, c, c2, aq4, sc4
         torch.cuda.empty_cache()
     return out
 
@@ -377,6 +384,15 @@ def main() -> int:
         d_mats = [lw["down"] for lw in layers]
 
         xq_d, sa_d = rt4_amd.quant_act_a8(x_d)
+        aq_gu, sa4_gu = rt4_amd.quant_act_a4(x_gu)
+
+        def gemv4_gu():
+            for wq, ws in gu_mats:
+                rt4_amd.gemv_w4a4_q(wq, ws, aq_gu, sa4_gu, out=y_g)
+
+        g4_us = timed_graph(torch, gemv4_gu) * 1e3 / len(gu_mats)
+        g4_bytes = Ngu * Kgu // 2 + Ngu * (Kgu // 128) * 2 + M * Kgu // 2 + M * (Kgu // 32) * 4 + M * Ngu * 4
+        kernels["gemv_w4a4_gate_up_m4"] = {"us": round(g4_us, 3), "GBs": round(g4_bytes / g4_us / 1e3, 1)}
 
         def gemv_d():
             for wq, ws in d_mats:

@@ -36,6 +36,14 @@ void k_quant_rows_a8(u32* qh, u32* ql, float* sc, float* sc16, const float* x, i
 void k_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int in_stride = 0,
                   int in_off = 0);
 
+// src/kernels.h:25 -- W4A4 decode GEMV (RT_ACT4 path), rows <= 4: activations
+// quantized to int4 per 32 elements, then the GEMV.
+void k_gemv_w4a4(float* y, const u32* wq, const float* wsc, const float* x, int rows, int N, int K);
+
+// src/kernels.h:29 -- int4 x int4 prefill GEMM on activations from k_quant_rows.
+void k_gemm_i4(float* c, const u32* wq, const float* wsc_gm, const u32* aq, const float* asc_gm,
+               int M, int N, int K);
+
 // src/kernels.h:40 -- Q quantizer of all heads for the attention kernel.
 void k_attn_q_quant(u32* qq, float* qs, const float* x, int T, int H, int D, int G, int TP);
 

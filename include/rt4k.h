@@ -197,12 +197,41 @@ int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, 
                               int off, int n_tile, int n_heads, int ratio, int kv_cap, int kv_splits,
                               void* stream);
 
-/* ------------------------------------------- W4A4 siblings (link only) ---- */
+/* ----------------------------------------- W4A4 siblings (RT_ACT4 path) ---- */
 
 /* int4 activation quantizer.  Replaces k_quant_rows (src/kernels.h:36,
  * src/k_new.hip:192-219): q uint32 [rows][K/8], sc f32 [K/G][rows], s = amax/7. */
 int rt4_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
                       int in_stride, int in_off, void* stream);
+
+/* Decode int4 activation quantizer, the first launch of k_gemv_w4a4 (quant_act4,
+ * kernels/gemv_w4a4_core.h:22-44): per (row, 32-element subgroup)
+ * s = amax>0 ? amax/7 : 1, q = clamp(lrintf(x/s), -8, 7).  aq uint32 [rows][K/8]
+ * (RT4 nibble order), sa f32 [rows][K/32].  K % 32 == 0. */
+int rt4_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, void* stream);
+
+/* W4A4 GEMV on quantized activations (gemv_w4a4, kernels/gemv_w4a4_core.h:47-132):
+ * y f32 [rows][N] = Σ_j f16(ws[n][j/4]) * sa[m][j] * Σ_{k∈j} code[n][k]*acode[m][k]
+ * over the 32-element subgroups j.  rows in [1,4], K % 128 == 0. */
+int rt4_gemv_w4a4_q(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int rows,
+                    int N, int K, void* stream);
+
+/* The whole W4A4 decode linear: quantize x, then the GEMV.  Replaces k_gemv_w4a4
+ * (src/kernels.h:25, src/k_gemv.hip:14-42).  The quantized activations go to
+ * library scratch grown with hipMalloc (as the reference does, :16-23).  The
+ * reference checks only rows <= 4; K % 128 == 0 is required here (the RT4 scale
+ * layout has one scale per 128 weights). */
+int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
+                  void* stream);
+
+/* int4 x int4 prefill GEMM.  Replaces k_gemm_i4 (src/kernels.h:29,
+ * src/k_gemm.hip:8-17): C f32 [M][N] = Σ_g I_g * asc_gm[g][m] * wsc_gm[g][n] with
+ * I_g = Σ_{k∈g} code_w*code_a exact.  aq uint32 [M][K/8] int4 codes (from
+ * k_quant_rows with G = 128), asc_gm f32 [K/128][M].  M % 128, N % 64, K % 128 == 0,
+ * as the reference requires.  The codes are sign-extended to int8 in library
+ * scratch and run through the W4A8 GEMM kernel (same integers per group). */
+int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint32_t* aq, const float* asc_gm, int M,
+                  int N, int K, void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

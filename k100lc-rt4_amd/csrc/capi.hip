@@ -327,6 +327,65 @@ int rt4_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, i
                       "rt4_quant_rows_a4 launch");
 }
 
+int rt4_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, void* stream) {
+    if (!aq || !sa || !x) return fail(RT4_E_ARG, "rt4_quant_act_a4: null pointer");
+    if (rows < 1 || rows > 65535) return fail(RT4_E_SHAPE, "rt4_quant_act_a4: rows=%d", rows);
+    if (K <= 0 || K % 32) return fail(RT4_E_SHAPE, "rt4_quant_act_a4: K=%d is not a positive multiple of 32", K);
+    if (!aligned(aq, 4) || !aligned(x, 4) || !aligned(sa, 4))
+        return fail(RT4_E_ARG, "rt4_quant_act_a4: misaligned pointer");
+    return hip_status(rt4::launch_quant_act_a4(aq, sa, x, rows, K, as_stream(stream)), "rt4_quant_act_a4 launch");
+}
+
+int rt4_gemv_w4a4_q(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int rows,
+                    int N, int K, void* stream) {
+    if (!y || !wq || !ws || !aq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a4: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_w4a4", rows, N, K);
+    if (rc) return rc;
+    if (!aligned(wq, 16) || !aligned(aq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a4: misaligned pointer (wq and aq need 16 bytes)");
+    return hip_status(rt4::launch_gemv_w4a4(y, wq, ws, aq, sa, rows, N, K, as_stream(stream)), "rt4_gemv_w4a4 launch");
+}
+
+int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
+                  void* stream) {
+    if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "k_gemv_w4a4: null pointer");
+    int rc = check_gemv_shape("k_gemv_w4a4", rows, N, K);
+    if (rc) return rc;
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
+        return fail(RT4_E_ARG, "k_gemv_w4a4: misaligned pointer (wq needs 16 bytes)");
+    void *q = nullptr, *s = nullptr;
+    if ((rc = scratch(kSlotActQ, (size_t)rows * K / 2, &q))) return rc;
+    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 32) * sizeof(float), &s))) return rc;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = rt4::launch_quant_act_a4(static_cast<uint32_t*>(q), static_cast<float*>(s), x, rows, K, st);
+    if (e != hipSuccess) return hip_status(e, "k_gemv_w4a4 quant launch");
+    return hip_status(rt4::launch_gemv_w4a4(y, wq, ws, static_cast<const uint32_t*>(q), static_cast<const float*>(s),
+                                            rows, N, K, st),
+                      "k_gemv_w4a4 launch");
+}
+
+int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint32_t* aq, const float* asc_gm, int M,
+                  int N, int K, void* stream) {
+    if (!c || !wq || !wsc_gm || !aq || !asc_gm) return fail(RT4_E_ARG, "k_gemm_i4: null pointer");
+    // the reference's tile preconditions (src/k_gemm.hip:10-14)
+    if (M <= 0 || N <= 0 || K <= 0 || M % 128 || N % 64 || K % 128)
+        return fail(RT4_E_SHAPE, "k_gemm_i4: shape must be multiples of BM=128/BN=64/G=128 (M=%d N=%d K=%d)", M, N,
+                    K);
+    int rc = check_gemm_args("k_gemm_i4", M, N, K);
+    if (rc) return rc;
+    if (!aligned(aq, 4) || !aligned(wq, 16) || !aligned(c, 4) || !aligned(asc_gm, 4) || !aligned(wsc_gm, 4))
+        return fail(RT4_E_ARG, "k_gemm_i4: misaligned pointer");
+    // The same per-group integers as the reference's int4 x int4 contraction, from
+    // the codes sign-extended to int8 (library scratch: the caller hands over no
+    // buffer for them).
+    void* q = nullptr;
+    if ((rc = scratch(kSlotGemmA, (size_t)M * K, &q))) return rc;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), nullptr, aq, M, K, st);
+    if (e != hipSuccess) return hip_status(e, "k_gemm_i4 code expansion");
+    return run_gemm("k_gemm_i4 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), asc_gm, M, N, K, st);
+}
+
 
 int rt4_gemm_w4a8_i8(float* c, const uint32_t* wq, const float* wsc_gm, const int8_t* xq,
                      const float* sc, int M, int N, int K, void* stream) {

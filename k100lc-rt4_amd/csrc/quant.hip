@@ -196,12 +196,13 @@ __device__ __forceinline__ uint32_t swar_sub8(uint32_t x) {
     return ((x | 0x80808080u) - 0x08080808u) ^ (~x & 0x80808080u);
 }
 
+template <bool HAS_H>
 __global__ __launch_bounds__(256) void hl_to_i8_k(const uint32_t* __restrict__ qh,
                                                   const uint32_t* __restrict__ ql,
                                                   int8_t* __restrict__ xq, size_t ndw) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= ndw) return;
-    const uint32_t h = qh[i], l = ql[i] ^ 0x88888888u;
+    const uint32_t h = HAS_H ? qh[i] : 0u, l = ql[i] ^ 0x88888888u;
     const uint32_t xe = ((h << 4) & 0xF0F0F0F0u) | (l & 0x0F0F0F0Fu);
     const uint32_t xo = (h & 0xF0F0F0F0u) | ((l >> 4) & 0x0F0F0F0Fu);
     reinterpret_cast<uint2*>(xq)[i] = make_uint2(swar_sub8(xe), swar_sub8(xo));
@@ -211,7 +212,42 @@ hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, i
                            hipStream_t st) {
     const size_t ndw = (size_t)rows * (K / 8);
     const unsigned blocks = (unsigned)((ndw + 255) / 256);
-    hipLaunchKernelGGL(hl_to_i8_k, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
+    if (qh)
+        hipLaunchKernelGGL(hl_to_i8_k<true>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
+    else  // int4 codes alone (W4A4): sign-extended into the same interleaved int8 order
+        hipLaunchKernelGGL(hl_to_i8_k<false>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Decode int4 activation quantizer (restates quant_act4, kernels/gemv_w4a4_core.h:
+// 22-44): per (row, 32-element subgroup) s = amax>0 ? amax/7 : 1,
+// q = clamp(lrintf(x/s), -8, 7).  Outputs codes u32 [rows][K/8] in the RT4
+// nibble order (low nibble = even k) and scales f32 [rows][K/32].  One lane per
+// 8 elements (one output dword); a subgroup is 4 lanes.  grid (ceil(K/8/256), rows).
+__global__ __launch_bounds__(256) void quant_act_a4_k(const float* __restrict__ x, uint32_t* __restrict__ aq,
+                                                      float* __restrict__ sa, int K, int x_aligned) {
+    const int m = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= (K >> 3)) return;                     // K%32==0: whole 4-lane runs exit together
+    float v[8];
+    load8(x + (size_t)m * K + 8 * (size_t)i, x_aligned, v);
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    amax = run_max<4>(amax);
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) w |= ((uint32_t)clampi((int)lrintf(v[e] / s), -8, 7) & 0xFu) << (4 * e);
+    aq[(size_t)m * (K >> 3) + i] = w;
+    if ((i & 3) == 0) sa[(size_t)m * (K >> 5) + (i >> 2)] = s;
+}
+
+hipError_t launch_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, hipStream_t st) {
+    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int aligned = ((uintptr_t)x & 15) == 0;
+    hipLaunchKernelGGL(quant_act_a4_k, grid, dim3(256), 0, st, x, aq, sa, K, aligned);
     return hipGetLastError();
 }
 

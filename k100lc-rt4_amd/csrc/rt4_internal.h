@@ -16,8 +16,10 @@ hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc
                                 hipStream_t st);
 hipError_t launch_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
                                 int in_stride, int in_off, hipStream_t st);
+// q8 = 16h + l from digit planes, or the sign-extended l alone when qh is null.
 hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
                            hipStream_t st);
+hipError_t launch_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, hipStream_t st);
 hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG, hipStream_t st);
 
 // ---- decode GEMV (gemv.hip)
@@ -45,6 +47,11 @@ size_t gemv_part_bytes(const GemvSplit& sp, int rows);
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,
                             const int8_t* xq, const float* sa, const float* xf, int rows, int N, int K,
                             const GemvCfg& cfg, const GemvSplit& sp, hipStream_t st);
+
+// ---- W4A4 decode GEMV (gemv4.hip): y f32 [rows][N] from RT4 weights and int4
+// activation codes aq u32 [rows][K/8] with scales sa f32 [rows][K/32]
+hipError_t launch_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
+                            int rows, int N, int K, hipStream_t st);
 
 // ---- prefill GEMM (gemm.hip)
 // C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],

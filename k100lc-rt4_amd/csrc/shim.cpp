@@ -35,6 +35,18 @@ void k_quant_rows(u32* q, float* sc, const float* x, int rows, int K, int G, int
         die("k_quant_rows");
 }
 
+// src/k_gemv.hip:14-42
+void k_gemv_w4a4(float* y, const u32* wq, const float* wsc, const float* x, int rows, int N, int K) {
+    if (rt4_gemv_w4a4(y, wq, reinterpret_cast<const uint16_t*>(wsc), x, rows, N, K, nullptr) != RT4_OK)
+        die("k_gemv_w4a4");
+}
+
+// src/k_gemm.hip:8-17
+void k_gemm_i4(float* c, const u32* wq, const float* wsc_gm, const u32* aq, const float* asc_gm, int M, int N,
+               int K) {
+    if (rt4_gemm_w4a4(c, wq, wsc_gm, aq, asc_gm, M, N, K, nullptr) != RT4_OK) die("k_gemm_i4");
+}
+
 // src/k_gemm.hip:22-34
 void k_gemm_i4_a8(float* c, float* c2, const u32* wq, const float* wsc_gm, const u32* ah,
                   const u32* al, const float* sc, const float* sc16, int M, int N, int K) {

@@ -31,7 +31,8 @@ C_EXPORTS = (
     "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
     "rt4_gemv_w4a8_groupsums",
     "rt4_gemv_w4a8", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
-    "rt4_make_group_major", "rt4_quant_rows_a4",
+    "rt4_make_group_major", "rt4_quant_rows_a4", "rt4_quant_act_a4", "rt4_gemv_w4a4_q", "rt4_gemv_w4a4",
+    "rt4_gemm_w4a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
     "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
     "rt4_attention_prefill_cfg",
@@ -46,6 +47,8 @@ CXX_EXPORTS = (
     "_Z13k_kv_append_kPjPfPKfiiiiii",
     "_Z13k_kv_append_vPjPfS0_PKfiiiiii",
     "_Z11k_attentionPfPKjPKfS1_S3_S1_S3_iiiiiiiiS_S_S_i",
+    "_Z11k_gemv_w4a4PfPKjPKfS3_iii",
+    "_Z9k_gemm_i4PfPKjPKfS1_S3_iii",
 )
 
 
@@ -58,6 +61,10 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGS = {
     "rt4_quant_act_a8": [_P, _P, _P, _P, _I, _I, _P],
+    "rt4_quant_act_a4": [_P, _P, _P, _I, _I, _P],
+    "rt4_gemv_w4a4_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a4": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemm_w4a4": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "rt4_gemv_launch_plan": [_I, _I, _I, _P, _P, _P],
@@ -258,6 +265,48 @@ def quant_rows_a4(x, rows: int | None = None, K: int | None = None, G: int = GRO
     _check(lib().rt4_quant_rows_a4(_ptr(q), _ptr(sc), _ptr(x), rows, K, G, in_stride, in_off,
                                    _stream()))
     return q, sc
+
+
+def quant_act_a4(x):
+    """Decode int4 quantizer of k_gemv_w4a4: x f32 [rows, K] -> (aq int32 [rows, K/8],
+    sa f32 [rows, K/32])."""
+    torch = _torch()
+    rows, K = x.shape
+    aq = _empty((rows, K // 8), torch.int32, x.device)
+    sa = _empty((rows, K // 32), torch.float32, x.device)
+    _check(lib().rt4_quant_act_a4(_ptr(aq), _ptr(sa), _ptr(x), rows, K, _stream()))
+    return aq, sa
+
+
+def gemv_w4a4_q(wq, ws, aq, sa, out=None):
+    """W4A4 GEMV on int4 activation codes aq int32 [rows, K/8], sa f32 [rows, K/32]."""
+    torch = _torch()
+    rows, KD = aq.shape
+    N = wq.shape[0]
+    y = out if out is not None else _empty((rows, N), torch.float32, aq.device)
+    _check(lib().rt4_gemv_w4a4_q(_ptr(y), _ptr(wq), _ptr(ws), _ptr(aq), _ptr(sa), rows, N, KD * 8, _stream()))
+    return y
+
+
+def gemv_w4a4(wq, ws, x, out=None):
+    """Drop-in k_gemv_w4a4: quantize x f32 [rows, K] to int4 per 32 and multiply (rows <= 4)."""
+    torch = _torch()
+    rows, K = x.shape
+    N = wq.shape[0]
+    y = out if out is not None else _empty((rows, N), torch.float32, x.device)
+    _check(lib().rt4_gemv_w4a4(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, _stream()))
+    return y
+
+
+def gemm_w4a4(wq, wsc_gm, aq, asc_gm, out=None):
+    """Drop-in k_gemm_i4: aq int32 [M, K/8] (k_quant_rows codes), asc_gm f32 [K/128, M],
+    wq int32 [N, K/8], wsc_gm f32 [K/128, N] -> c f32 [M, N]."""
+    torch = _torch()
+    M, KD = aq.shape
+    N = wq.shape[0]
+    c = out if out is not None else _empty((M, N), torch.float32, aq.device)
+    _check(lib().rt4_gemm_w4a4(_ptr(c), _ptr(wq), _ptr(wsc_gm), _ptr(aq), _ptr(asc_gm), M, N, KD * 8, _stream()))
+    return c
 
 
 def gemm_w4a8_i8(wq, wsc_gm, xq, sc, out=None):

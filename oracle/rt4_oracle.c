@@ -25,6 +25,10 @@
  *   rt4o_quant_rows_a4  closed form + reference GPU build
  *   rt4o_gemv_*         brute-force integer dot, Σu·a-8Σa identity
  *                       (kernels/gemv_int4.hip:317-336), fp64 fold
+ *   rt4o_quant_act4     closed form + invariants (|q|<=8, argmax -> +-7, zero
+ *                       subgroup -> s=1) + numpy restatement + the reference's
+ *                       quant_act4 built for gfx950 (GPU test)
+ *   rt4o_gemv_w4a4_*    brute-force integer dots (numpy), fp64 fold
  *   rt4o_gemm_*         per-group int = 16*I_h + I_l identity, fp64 fold as in
  *                       bench/int4_gemm2.cpp:104-123
  *   rt4o_quant_weight_rows, rt4o_f32_to_f16_conv
@@ -342,6 +346,79 @@ void rt4o_gemv_w4a8(const uint32_t* wq, const uint16_t* ws, const float* x, int 
     rt4o_gemv_groupsums(wq, q, M, N, K, I);
     rt4o_gemv_fold(I, ws, sa, M, N, K, y);
     free(q);
+    free(sa);
+    free(I);
+}
+
+/* ------------------------------------------------------------- W4A4 GEMV -- */
+#define RT4O_SG 32
+
+/* Decode int4 activation quantizer, restating quant_act4
+ * (kernels/gemv_w4a4_core.h:22-44): per (row m, 32-element subgroup j)
+ * s = amax>0 ? amax/7 : 1, q = clamp(lrintf(x/s), -8, 7); codes packed 8 per
+ * dword in the RT4 order (low nibble = even k), scales sa[m][j]. */
+void rt4o_quant_act4(const float* x, int M, int K, uint32_t* aq, float* sa) {
+    const int NS = K / RT4O_SG;
+    for (int m = 0; m < M; m++)
+        for (int j = 0; j < NS; j++) {
+            const float* src = x + (size_t)m * K + (size_t)j * RT4O_SG;
+            float amax = 0.f;
+            for (int i = 0; i < RT4O_SG; i++) amax = fmaxf(amax, fabsf(src[i]));
+            const float s = amax > 0.f ? amax / 7.f : 1.f;
+            sa[(size_t)m * NS + j] = s;
+            for (int d = 0; d < RT4O_SG / 8; d++) {
+                uint32_t w = 0;
+                for (int e = 0; e < 8; e++) {
+                    int c = (int)lrintf(src[8 * d + e] / s);
+                    c = c > 7 ? 7 : (c < -8 ? -8 : c);
+                    w |= ((uint32_t)c & 0xFu) << (4 * e);
+                }
+                aq[(size_t)m * (K / 8) + (size_t)j * 4 + d] = w;
+            }
+        }
+}
+
+/* Exact per-subgroup dots of the W4A4 GEMV: I[m][n][j] = Σ_{k in subgroup j}
+ * code[n][k] * acode[m][k] (gemv_w4a4, kernels/gemv_w4a4_core.h:101-110, four
+ * v_dot8 per lane = one 32-element subgroup). */
+void rt4o_gemv_w4a4_sums(const uint32_t* wq, const uint32_t* aq, int M, int N, int K, int32_t* I) {
+    const int NS = K / RT4O_SG, KD = K / 8;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; n++)
+        for (int m = 0; m < M; m++)
+            for (int j = 0; j < NS; j++) {
+                int32_t s = 0;
+                for (int d = 4 * j; d < 4 * j + 4; d++) s = rt4o_dot8_i4(aq[(size_t)m * KD + d], wq[(size_t)n * KD + d], s);
+                I[((size_t)m * N + n) * NS + j] = s;
+            }
+}
+
+/* fp64 fold: y[m][n] = Σ_j f16(ws[n][j/4]) * sa[m][j] * I[m][n][j]
+ * (kernels/gemv_w4a4_core.h:111-117: weight group scale per 128, activation
+ * scale per 32). */
+void rt4o_gemv_w4a4_fold(const int32_t* I, const uint16_t* ws, const float* sa, int M, int N, int K, double* y) {
+    const int NS = K / RT4O_SG, NG = K / RT4O_GROUP;
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; n++)
+        for (int m = 0; m < M; m++) {
+            double acc = 0.0;
+            for (int j = 0; j < NS; j++)
+                acc += (double)rt4o_f16_to_f32(ws[(size_t)n * NG + j / 4]) * (double)sa[(size_t)m * NS + j] *
+                       (double)I[((size_t)m * N + n) * NS + j];
+            y[(size_t)m * N + n] = acc;
+        }
+}
+
+/* The whole W4A4 decode linear as k_gemv_w4a4 does it (src/k_gemv.hip:14-42). */
+void rt4o_gemv_w4a4(const uint32_t* wq, const uint16_t* ws, const float* x, int M, int N, int K, double* y) {
+    const int NS = K / RT4O_SG;
+    uint32_t* aq = (uint32_t*)malloc((size_t)M * (K / 8) * sizeof(uint32_t));
+    float* sa = (float*)malloc((size_t)M * NS * sizeof(float));
+    int32_t* I = (int32_t*)malloc((size_t)M * N * NS * sizeof(int32_t));
+    rt4o_quant_act4(x, M, K, aq, sa);
+    rt4o_gemv_w4a4_sums(wq, aq, M, N, K, I);
+    rt4o_gemv_w4a4_fold(I, ws, sa, M, N, K, y);
+    free(aq);
     free(sa);
     free(I);
 }

@@ -48,6 +48,10 @@ def lib() -> ctypes.CDLL:
             "rt4o_gemv_w4a8": ([P, P, P, I, I, I, P], None),
             "rt4o_gemm_w4a8_points": ([P, P, P, P, P, P, I, I, I, P, P, I, P, P], None),
             "rt4o_gemm_w4a4_points": ([P, P, P, P, I, I, I, P, P, I, P, P], None),
+            "rt4o_quant_act4": ([P, I, I, P, P], None),
+            "rt4o_gemv_w4a4_sums": ([P, P, I, I, I, P], None),
+            "rt4o_gemv_w4a4_fold": ([P, P, P, I, I, I, P], None),
+            "rt4o_gemv_w4a4": ([P, P, P, I, I, I, P], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -176,6 +180,49 @@ def gemv_w4a8(wq: np.ndarray, ws: np.ndarray, x: np.ndarray) -> np.ndarray:
     N = wq.shape[0]
     y = np.empty((M, N), np.float64)
     lib().rt4o_gemv_w4a8(_p(wq), _p(ws), _p(x), M, N, K, _p(y))
+    return y
+
+
+SG = 32
+
+
+def quant_act4(x: np.ndarray):
+    """quant_act4 (kernels/gemv_w4a4_core.h:22-44): -> (aq uint32 [M, K/8], sa f32 [M, K/32])."""
+    x = _c(x, np.float32)
+    M, K = x.shape
+    aq = np.empty((M, K // 8), np.uint32)
+    sa = np.empty((M, K // SG), np.float32)
+    lib().rt4o_quant_act4(_p(x), M, K, _p(aq), _p(sa))
+    return aq, sa
+
+
+def gemv_w4a4_sums(wq: np.ndarray, aq: np.ndarray) -> np.ndarray:
+    """Exact I[m][n][j] over 32-element subgroups (int4 x int4)."""
+    wq = _c(wq, np.uint32)
+    aq = _c(aq, np.uint32)
+    M, KD = aq.shape
+    N = wq.shape[0]
+    I = np.empty((M, N, KD * 8 // SG), np.int32)
+    lib().rt4o_gemv_w4a4_sums(_p(wq), _p(aq), M, N, KD * 8, _p(I))
+    return I
+
+
+def gemv_w4a4_fold(I: np.ndarray, ws: np.ndarray, sa: np.ndarray) -> np.ndarray:
+    """fp64 Σ_j f16(ws[n][j/4])*sa[m][j]*I[m][n][j]."""
+    I = _c(I, np.int32)
+    M, N, NS = I.shape
+    y = np.empty((M, N), np.float64)
+    lib().rt4o_gemv_w4a4_fold(_p(I), _p(_c(ws, np.uint16)), _p(_c(sa, np.float32)), M, N, NS * SG, _p(y))
+    return y
+
+
+def gemv_w4a4(wq: np.ndarray, ws: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """k_gemv_w4a4 (src/k_gemv.hip:14-42) end to end, fp64 result."""
+    x = _c(x, np.float32)
+    M, K = x.shape
+    N = wq.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().rt4o_gemv_w4a4(_p(_c(wq, np.uint32)), _p(_c(ws, np.uint16)), _p(x), M, N, K, _p(y))
     return y
 
 

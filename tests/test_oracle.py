@@ -254,3 +254,75 @@ def test_gemm_w4a4_points(orc):
     c, Ig = orc.gemm_w4a4_points(wq, sb, aq, sa, M, N, K, mi, ni)
     I = np_ref.gemv_groupsums(codes, layout.unpack_rt4(aq))
     assert np.array_equal(Ig.reshape(M, N, -1), I)
+
+
+# ------------------------------------------------------------- W4A4 GEMV ----
+def _np_quant_act4(x):
+    """quant_act4 (kernels/gemv_w4a4_core.h:22-44) in numpy: per 32 elements
+    s = amax/7 (fp32 division), q = clip(rint(x/s), -8, 7) (round half to even)."""
+    M, K = x.shape
+    xg = x.reshape(M, K // 32, 32)
+    amax = np.abs(xg).max(axis=2)
+    s = np.where(amax > 0, (amax / np.float32(7)).astype(np.float32), np.float32(1)).astype(np.float32)
+    q = np.clip(np.rint((xg / s[:, :, None]).astype(np.float32)), -8, 7).astype(np.int8).reshape(M, K)
+    return q, s
+
+
+def test_quant_act4_matches_numpy_and_invariants(orc):
+    rng = np.random.default_rng(31)
+    M, K = 4, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0, :32] = 0.0                                        # zero subgroup -> s = 1, q = 0
+    x[1, 32:64] = np.float32(-2.0)                          # constant subgroup -> all -7
+    x[2, 64:96] = np.minimum(np.arange(32, dtype=np.float32) * np.float32(0.5) - np.float32(7.0),
+                             np.float32(7.0))               # amax 7 -> s = 1: half-way points round to even
+    x[3, 96:128] *= np.float32(1e-30)
+    aq, sa = orc.quant_act4(x)
+    q = layout.unpack_rt4(aq)
+    q2, s2 = _np_quant_act4(x)
+    assert np.array_equal(q, q2) and np.array_equal(sa.view(np.uint32), s2.view(np.uint32))
+    assert sa[0, 0] == 1.0 and not q[0, :32].any()
+    assert (q[1, 32:64] == -7).all()
+    assert sa[2, 2] == 1.0
+    assert q[2, 64 + 1] == -6 and q[2, 64 + 3] == -6 and q[2, 64 + 5] == -4   # -6.5 -> -6, -5.5 -> -6, -4.5 -> -4
+    g = np.abs(x.reshape(M, K // 32, 32)).argmax(axis=2)
+    qq = q.reshape(M, K // 32, 32)
+    for m in range(M):
+        for j in range(K // 32):
+            if x[m, 32 * j:32 * j + 32].any():
+                assert abs(int(qq[m, j, g[m, j]])) == 7
+
+
+def test_quant_act4_brute_force_tiny(orc):
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((1, 32)).astype(np.float32)
+    amax = np.float32(0)
+    for v in x[0]:
+        amax = max(amax, np.float32(abs(v)))
+    s = np.float32(amax / np.float32(7))
+    expect = [max(-8, min(7, int(np.rint(np.float32(v / s))))) for v in x[0]]
+    aq, sa = orc.quant_act4(x)
+    assert layout.unpack_rt4(aq)[0].tolist() == expect and sa[0, 0] == s
+
+
+def test_gemv_w4a4_sums_and_fold(orc):
+    rng = np.random.default_rng(33)
+    M, N, K = 3, 48, 640
+    codes = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    ws = (np.abs(rng.standard_normal((N, K // 128))) * 0.01 + 1e-3).astype(np.float16)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    wq = layout.pack_rt4(codes)
+    aq, sa = orc.quant_act4(x)
+    a = layout.unpack_rt4(aq).astype(np.int64)
+    I = orc.gemv_w4a4_sums(wq, aq)
+    brute = np.einsum("mjk,njk->mnj", a.reshape(M, K // 32, 32), codes.astype(np.int64).reshape(N, K // 32, 32))
+    assert np.array_equal(I, brute)
+    y = orc.gemv_w4a4(wq, ws.view(np.uint16), x)
+    deq_a = a.reshape(M, K // 32, 32).astype(np.float64) * sa[:, :, None].astype(np.float64)
+    deq_w = codes.reshape(N, K // 128, 128).astype(np.float64) * ws.astype(np.float64)[:, :, None]
+    ref = deq_a.reshape(M, K) @ deq_w.reshape(N, K).T
+    assert np.allclose(y, ref, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(orc.gemv_w4a4_fold(I, ws.view(np.uint16), sa), y)
+    # a plausible mistake -- one activation scale per 128 instead of per 32 -- must show
+    sa_bad = np.repeat(sa[:, ::4], 4, axis=1)
+    assert not np.allclose(orc.gemv_w4a4_fold(I, ws.view(np.uint16), sa_bad), y, rtol=1e-6)
