@@ -62,6 +62,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8, help="distinct weight sets rotated through")
+    ap.add_argument("--rt4", metavar="MANIFEST", default=None,
+                    help="decode step on the MLP weights of an RT4 file (converter manifest) instead of "
+                         "synthetic ones; the kernel table and CPU baseline are skipped")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-kernel table beyond the roofline")
@@ -199,6 +202,35 @@ def gemm_table(torch, rt4_amd, workload, gen) -> dict:
     return out
 
 
+def rt4_layers(rt4_amd, manifest: str, max_layers: int):
+    """The MLP projections of up to max_layers layers of an RT4 file, uploaded for the
+    kernels: ([{"gate", "up", "down"} -> (wq, ws)], (N, K) of gate/up, (N, K) of down)."""
+    from rt4_amd.rt4file import RT4File
+    f = RT4File(manifest)
+    names = set(f.names())
+    layers, shapes = [], None
+    i = 0
+    while len(layers) < max_layers:
+        pre = next((p for p in (f"model.language_model.layers.{i}.mlp.", f"model.layers.{i}.mlp.")
+                    if p + "gate_proj.weight" in names), None)
+        if pre is None:
+            if i > 4096:
+                break
+            i += 1
+            continue
+        lw = {k: f.upload(pre + f"{k}_proj.weight") for k in ("gate", "up", "down")}
+        s = (tuple(f.info(pre + "gate_proj.weight")["shape"]), tuple(f.info(pre + "down_proj.weight")["shape"]))
+        if shapes is None:
+            shapes = s
+        if s == shapes:
+            layers.append(lw)
+        i += 1
+    f.close()
+    if not layers:
+        raise SystemExit(f"bench.py: no layer with mlp.gate_proj/up_proj/down_proj in {manifest}")
+    return layers, shapes[0], shapes[1]
+
+
 def attn_table(torch, rt4_amd, workload, gen) -> dict:
     """int4-KV FlashAttention prefill: 24 query heads over 4 KV
     heads, head dim 256, 1024 new queries over a 32768-token cache, causal.  Effective
@@ -312,7 +344,13 @@ def main() -> int:
     (Ngu, Kgu), (Nd, Kd) = (17408, 5120), (5120, 17408)
     L = max(1, args.layers)
     layers = []
-    for _ in range(L):
+    rt4_source = None
+    if args.rt4:
+        layers, (Ngu, Kgu), (Nd, Kd) = rt4_layers(rt4_amd, args.rt4, L)
+        L = len(layers)
+        rt4_source = args.rt4
+        args.no_extra = args.no_cpu = True
+    for _ in range(L if not layers else 0):
         layers.append({k: workload.weights_torch(N, K, generator=gen)
                        for k, (N, K) in (("gate", (Ngu, Kgu)), ("up", (Ngu, Kgu)), ("down", (Nd, Kd)))})
     x_gu = workload.acts_torch(M, Kgu, generator=gen)
@@ -450,7 +488,8 @@ def main() -> int:
     out = {
         "metric": metric, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K_steps,
         "warmup": W_steps, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int4*int8->int32", "data": "synthetic",
+        "vs_baseline": None, "dtype": "int4*int8->int32",
+        "data": "synthetic" if rt4_source is None else f"RT4 file {rt4_source} (activations synthetic)",
         "config": {"workload": "decode MLP step, MTP3 verify width (BASELINE configs[1])", "M": M,
                    "gate_up_NK": [Ngu, Kgu], "down_NK": [Nd, Kd], "linears_per_step": 3,
                    "layers_rotated": L, "step_bytes": step_bytes, "graph_matches_eager": graph_ok,

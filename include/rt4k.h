@@ -233,6 +233,43 @@ int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float*
 int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint32_t* aq, const float* asc_gm, int M,
                   int N, int K, void* stream);
 
+/* ------------------------------------------------------------ RT4 files ---- */
+
+/* The converter's output (tools/convert.c:338-381, manifest :546-560) opened as
+ * the reference runtime does (RT4::load / RT4::upload, src/model.cpp:141-185):
+ * the manifest is parsed, the weight file memory-mapped read-only, every
+ * tensor's regions checked to lie inside it (and, for i4/i8, to start 256-byte
+ * aligned).  Handles are not thread-safe; host pointers stay valid until
+ * rt4_file_close. */
+typedef struct rt4_tensor_info {
+    const char* name;      /* owned by the file handle */
+    char kind[8];          /* "i4", "i8" (codes + fp16 group scales), or a plain kind ("f32", "f16", ...) */
+    int ndim;
+    int64_t shape[4];      /* i4/i8: [N, K] */
+    int64_t group;         /* scale group along K (128) */
+    int64_t q_off, s_off;  /* byte offsets of the codes (or the plain data) and of the scales (-1: none) */
+    int64_t q_bytes, s_bytes;
+    double relerr, src_rms;  /* the converter's quantization report */
+} rt4_tensor_info;
+
+/* Open a manifest; weight_path NULL uses its "weight_file" (tried as written,
+ * then next to the manifest). */
+int rt4_file_open(const char* manifest_path, const char* weight_path, void** file);
+int rt4_file_close(void* file);
+int rt4_file_count(void* file, int* count);
+int rt4_file_find(void* file, const char* name, int* index);
+int rt4_file_info(void* file, int index, rt4_tensor_info* info);
+/* Host pointers into the mapping (s is NULL for plain kinds). */
+int rt4_file_data(void* file, int index, const void** q, const void** s);
+int rt4_file_size(void* file, int64_t* bytes);
+/* The whole file into one device buffer of at least rt4_file_size bytes, in
+ * 256 MB pieces as src/model.cpp:178-184; a tensor then sits at dev + q_off /
+ * dev + s_off (wq and ws of the kernels here).  Returns after the copy. */
+int rt4_file_upload(void* file, void* dev, int64_t dev_bytes, void* stream);
+/* One tensor: codes to q_dev (q_bytes), scales to s_dev (s_bytes).  Returns
+ * after the copy. */
+int rt4_file_upload_tensor(void* file, int index, void* q_dev, void* s_dev, void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

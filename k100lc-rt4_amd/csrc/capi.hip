@@ -192,6 +192,10 @@ int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq,
 
 }  // namespace
 
+namespace rt4 {
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace rt4
+
 extern "C" {
 
 const char* rt4_last_error(void) { return g_err; }

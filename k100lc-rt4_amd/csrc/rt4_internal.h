@@ -7,6 +7,9 @@
 
 namespace rt4 {
 
+// Records msg as this thread's rt4_last_error() text and returns code.
+int set_error(int code, const char* msg);
+
 // ---- quantizers (quant.hip)
 hipError_t launch_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows,
                                int K, hipStream_t st);

@@ -36,6 +36,8 @@ C_EXPORTS = (
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
     "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
     "rt4_attention_prefill_cfg",
+    "rt4_file_open", "rt4_file_close", "rt4_file_count", "rt4_file_find", "rt4_file_info", "rt4_file_data",
+    "rt4_file_size", "rt4_file_upload", "rt4_file_upload_tensor",
 )
 # The reference-compatible C++ entry points (include/rt4_kernels.h), mangled.
 CXX_EXPORTS = (
