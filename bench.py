@@ -409,7 +409,8 @@ def main() -> int:
     gu_bytes = gemv_kernel_bytes(M, Ngu, Kgu)
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     plan = rt4_amd.gemv_launch_plan(M, Ngu, Kgu)
-    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{plan['groups_per_wave']},false,false> (gate/up GEMV, "
+    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{plan['groups_per_wave']},{plan['row_blocks']},false,false> "
+                          f"(gate/up GEMV, "
                           f"M={M} K={Kgu} N={Ngu}, "
                           f"{plan['waves']} waves/tile, {plan['k_splits']} K pieces/leftover tile)",
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

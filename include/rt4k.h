@@ -60,22 +60,26 @@ int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8
                     const float* sa, int rows, int N, int K, void* stream);
 
 /* Same, with an explicit launch configuration (tuning and tests).  A
- * workgroup owns one 16-row weight tile; groups_per_wave (even, 2..12) is the
- * number of 128-wide K groups each wave streams per pass, waves (1..16, at most
- * the number of such chunks) the waves per workgroup.  When the tile count is
- * not a multiple of the CU count, the leftover tiles can be cut along K into
- * pieces that run on otherwise idle CUs: k_splits 1 keeps every tile whole,
- * S >= 2 allows up to S pieces per leftover tile.  0 selects the default for
- * each parameter. */
+ * workgroup owns one tile of row_blocks x 16 weight rows (row_blocks 1 or 2:
+ * with 2 each wave applies its activations to two 16-row blocks);
+ * groups_per_wave (even, 2..12) is the number of 128-wide K groups each wave
+ * streams per pass, waves (1..16, at most the number of such chunks) the waves
+ * per workgroup.  When the tile count is not a multiple of the CU count, the
+ * leftover tiles can be cut along K into pieces that run on otherwise idle
+ * CUs: k_splits 1 keeps every tile whole, S >= 2 allows up to S pieces per
+ * leftover tile.  0 selects the default for each parameter.  Every
+ * configuration gives the same y bit for bit. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
-                        int k_splits, void* stream);
+                        int k_splits, int row_blocks, void* stream);
 
 /* The launch configuration rt4_gemv_w4a8_q picks for this shape on the
- * current device: groups per wave, waves per workgroup and the number of K
- * pieces per leftover tile (1: all tiles whole).  No counterpart in the
- * reference (its launch is fixed per M); for tuning and reports. */
-int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits);
+ * current device: groups per wave, waves per workgroup, the number of K
+ * pieces per leftover tile (1: all tiles whole) and the 16-row blocks per tile.
+ * No counterpart in the reference (its launch is fixed per M); for tuning and
+ * reports. */
+int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits,
+                         int* row_blocks);
 
 /* Test hook: the same kernel, also writing the exact per-group int32 dot
  * products gsum int32 [rows][N][K/128] = Σ_{k∈g} code[n][k]*xq[m][k]. */
@@ -98,7 +102,7 @@ int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float*
  * rt4_quant_act_a8, so y equals the two-launch result bit for bit.  No
  * library scratch.  x must be 16-byte aligned. */
 int rt4_gemv_w4a8_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
-                      int groups_per_wave, int waves, int k_splits, void* stream);
+                      int groups_per_wave, int waves, int k_splits, int row_blocks, void* stream);
 
 /* ----------------------------------------------------------- prefill path -- */
 

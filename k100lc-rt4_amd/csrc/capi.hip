@@ -141,10 +141,11 @@ int run_gemv(const char* who, int32_t* gsum, float* y, const uint32_t* wq, const
     rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
     if (sp.nrem > 0) {
         // Sized once for the largest split any shape can need (at most one piece
-        // per CU, 4 rows), so only the first split launch on a device allocates.
+        // per CU, 4 rows, two row blocks), so only the first split launch on a
+        // device allocates.
         // Under graph capture nothing may be allocated: if the workspace does not
         // exist yet, the launch runs unsplit (same results, less balanced).
-        const size_t pb = (size_t)cus * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
+        const size_t pb = (size_t)cus * rt4::kGemvMaxRb * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
         hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
         void *part = nullptr, *cnt = nullptr;
@@ -162,10 +163,20 @@ int run_gemv(const char* who, int32_t* gsum, float* y, const uint32_t* wq, const
     return hip_status(rt4::launch_gemv_w4a8(y, gsum, wq, ws, xq, sa, xf, rows, N, K, c, sp, st), who);
 }
 
+// The default launch configuration of a shape on the current device.
+int default_cfg(int rows, int N, int K, rt4::GemvCfg* out) {
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    *out = rt4::gemv_default_cfg(rows, N, K, cus);
+    return RT4_OK;
+}
+
 // Default launch configuration with the caller's overrides (0 keeps a default).
 int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int waves, int k_splits,
-             rt4::GemvCfg* out) {
-    rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+             int row_blocks, rt4::GemvCfg* out) {
+    // The overrides are checked before the device is queried (argument errors
+    // come first); only the default row-block count depends on the CU count.
+    rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K, 0);
     if (groups_per_wave > 0) {
         c.gpw = groups_per_wave;
         const int nc = (K / 128 + c.gpw - 1) / c.gpw;
@@ -173,9 +184,16 @@ int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int w
     }
     if (waves > 0) c.waves = waves;
     if (k_splits > 0) c.max_split = k_splits;
-    if (groups_per_wave < 0 || waves < 0 || k_splits < 0 || !rt4::gemv_cfg_valid(c, K))
-        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d", who, groups_per_wave,
-                    waves, k_splits);
+    if (row_blocks > 0) c.rb = row_blocks;
+    if (groups_per_wave < 0 || waves < 0 || k_splits < 0 || row_blocks < 0 || !rt4::gemv_cfg_valid(c, K))
+        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d row_blocks=%d", who,
+                    groups_per_wave, waves, k_splits, row_blocks);
+    if (row_blocks == 0) {
+        rt4::GemvCfg d;
+        int rc = default_cfg(rows, N, K, &d);
+        if (rc) return rc;
+        c.rb = d.rb;
+    }
     *out = c;
     return RT4_OK;
 }
@@ -214,31 +232,34 @@ int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int ro
 
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
-                        int k_splits, void* stream) {
+                        int k_splits, int row_blocks, void* stream) {
     if (!y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8", rows, N, K);
     if (rc || (rc = check_gemv_align("rt4_gemv_w4a8", y, wq, ws, xq, sa))) return rc;
     rt4::GemvCfg c;
-    if ((rc = gemv_cfg("rt4_gemv_w4a8", K, rows, N, groups_per_wave, waves, k_splits, &c))) return rc;
+    if ((rc = gemv_cfg("rt4_gemv_w4a8", K, rows, N, groups_per_wave, waves, k_splits, row_blocks, &c))) return rc;
     return run_gemv("rt4_gemv_w4a8 launch", nullptr, y, wq, ws, xq, sa, nullptr, rows, N, K, c, as_stream(stream));
 }
 
-int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits) {
-    if (!groups_per_wave || !waves || !k_splits) return fail(RT4_E_ARG, "rt4_gemv_launch_plan: null pointer");
+int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits,
+                         int* row_blocks) {
+    if (!groups_per_wave || !waves || !k_splits || !row_blocks)
+        return fail(RT4_E_ARG, "rt4_gemv_launch_plan: null pointer");
     int rc = check_gemv_shape("rt4_gemv_launch_plan", rows, N, K);
     int cus = 0;
     if (rc || (rc = device_cus(&cus))) return rc;
-    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K, cus);
     const rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
     *groups_per_wave = c.gpw;
     *waves = c.waves;
     *k_splits = sp.nrem > 0 ? sp.S : 1;
+    *row_blocks = c.rb;
     return RT4_OK;
 }
 
 int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                     const float* sa, int rows, int N, int K, void* stream) {
-    return rt4_gemv_w4a8_q_cfg(y, wq, ws, xq, sa, rows, N, K, 0, 0, 0, stream);
+    return rt4_gemv_w4a8_q_cfg(y, wq, ws, xq, sa, rows, N, K, 0, 0, 0, 0, stream);
 }
 
 int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws,
@@ -247,20 +268,22 @@ int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const u
     if (!gsum || !y || !wq || !ws || !xq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a8_groupsums: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8_groupsums", rows, N, K);
     if (rc || (rc = check_gemv_align("rt4_gemv_w4a8_groupsums", y, wq, ws, xq, sa))) return rc;
-    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    rt4::GemvCfg c;
+    if ((rc = default_cfg(rows, N, K, &c))) return rc;
     return run_gemv("rt4_gemv_w4a8_groupsums launch", gsum, y, wq, ws, xq, sa, nullptr, rows, N, K, c,
                     as_stream(stream));
 }
 
 int rt4_gemv_w4a8_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
-                      int groups_per_wave, int waves, int k_splits, void* stream) {
+                      int groups_per_wave, int waves, int k_splits, int row_blocks, void* stream) {
     if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8_cfg", rows, N, K);
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 16) || !aligned(ws, 2))
         return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: misaligned pointer (wq and x need 16 bytes)");
     rt4::GemvCfg c;
-    if ((rc = gemv_cfg("rt4_gemv_w4a8_cfg", K, rows, N, groups_per_wave, waves, k_splits, &c))) return rc;
+    if ((rc = gemv_cfg("rt4_gemv_w4a8_cfg", K, rows, N, groups_per_wave, waves, k_splits, row_blocks, &c)))
+        return rc;
     return run_gemv("rt4_gemv_w4a8_cfg launch", nullptr, y, wq, ws, nullptr, nullptr, x, rows, N, K, c,
                     as_stream(stream));
 }
@@ -272,10 +295,11 @@ int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
         return fail(RT4_E_ARG, "k_gemv_w4a8: misaligned pointer (wq needs 16 bytes)");
-    const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K);
+    rt4::GemvCfg c;
+    if ((rc = default_cfg(rows, N, K, &c))) return rc;
     // Two launches, as the reference: the activation quantizer into library
     // scratch, then the GEMV.  (The fused one-launch form, rt4_gemv_w4a8_cfg,
-    // re-quantizes the activations in every 16-row tile and measures slower.)
+    // re-quantizes the activations in every tile and measures slower.)
     void *q = nullptr, *s = nullptr;
     if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q))) return rc;
     if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s))) return rc;

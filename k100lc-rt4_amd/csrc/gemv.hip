@@ -8,9 +8,13 @@
 // 44.5 MB per 27B MLP matrix against a few KB of activations, so its layout is
 // chosen for the memory system first.
 //
-// * Work split: a workgroup owns one 16-row weight tile; its W waves split the
-//   K groups of that tile, GPW groups (an even number) each.  Every wave issues
-//   all of its loads up front; W*GPW*16 rows x 64 B is the tile's full K.
+// * Work split: a workgroup owns one tile of RB x 16 weight rows; its W waves
+//   split the K groups of that tile, GPW groups (an even number) each.  Every
+//   wave issues all of its loads up front.  With RB = 2 a wave multiplies one
+//   activation operand into two 16-row blocks, which halves the activation
+//   reloads per weight byte; it pays where the tile count is many times the CU
+//   count (the LM head), and loses where the grid would be only a few tiles per
+//   CU (load imbalance in the last round).
 // * Weight loads: one dwordx4 load instruction covers 8 rows x 128 B, i.e. 8
 //   whole cache lines (two 128-element groups of 8 rows).  A 16-row MFMA tile
 //   would otherwise read 16 half lines per instruction, which measured ~25%
@@ -130,7 +134,7 @@ __device__ __forceinline__ float load_dev(const float* p) {
     return v;
 }
 
-template <int M, int GPW, bool GSUM, bool QIN>
+template <int M, int GPW, int RB, bool GSUM, bool QIN>
 __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
                                                     const int8_t* __restrict__ xq,
@@ -155,51 +159,62 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     const int rem = piece ? b / sp.S : 0, pc = piece ? b % sp.S : 0;
     const int tile = piece ? sp.full + rem : b - npieces;
     const int c_lo = piece ? pc * NC / sp.S : 0, c_hi = piece ? (pc + 1) * NC / sp.S : NC;
-    const int n0 = tile * 16;
-    // scale slice of this wave: [16 rows][GPW/2] dwords (fp16 pairs), then the
-    // reduction area; always accessed as dwords
-    uint32_t* wsl = reinterpret_cast<uint32_t*>(smem) + (size_t)w * 8 * GPW;
-    float* red = reinterpret_cast<float*>(smem + (size_t)W * 16 * GPW * 2);
+    const int n0 = tile * 16 * RB;
+    // scale slice of this wave: [RB][16 rows][GPW/2] dwords (fp16 pairs), then
+    // the reduction area [W][RB][M][16]; always accessed as dwords
+    uint32_t* wsl = reinterpret_cast<uint32_t*>(smem) + (size_t)w * 8 * GPW * RB;
+    float* red = reinterpret_cast<float*>(smem + (size_t)W * 16 * GPW * 2 * RB);
 
     // Load mapping of a group pair (rows n0..n0+15, 128 B each):
     //   instruction 1 covers rows 0-7, instruction 2 rows 8-15, 8 lanes per row;
     //   lane (j<8, q):  inst1 = (row j,    chunk q),   inst2 = (row j+8, chunk 4+q)
     //   lane (j>=8, q): inst1 = (row j-8,  chunk 4+q), inst2 = (row j,   chunk q)
     // so the first group of the pair is sel(j<8 ? inst1 : inst2) and the second
-    // is ror8(sel(j<8 ? inst2 : inst1)).
+    // is ror8(sel(j<8 ? inst2 : inst1)).  Row block rb covers rows n0 + 16 rb ...
     const bool lo = j < 8;
-    int r1 = n0 + (lo ? j : j - 8), r2 = n0 + (lo ? j + 8 : j);
-    r1 = r1 < N ? r1 : N - 1;                    // tail rows read a valid row; dropped
-    r2 = r2 < N ? r2 : N - 1;
-    const unsigned char* p1 = reinterpret_cast<const unsigned char*>(wq) + (size_t)r1 * RS + (lo ? q : 4 + q) * 16;
-    const unsigned char* p2 = reinterpret_cast<const unsigned char*>(wq) + (size_t)r2 * RS + (lo ? 4 + q : q) * 16;
-    const int rj = n0 + j < N ? n0 + j : N - 1;
+    const unsigned char* p1[RB];
+    const unsigned char* p2[RB];
+    int rj[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        const int nb = n0 + 16 * rb;
+        int r1 = nb + (lo ? j : j - 8), r2 = nb + (lo ? j + 8 : j);
+        r1 = r1 < N ? r1 : N - 1;                // tail rows read a valid row; dropped
+        r2 = r2 < N ? r2 : N - 1;
+        p1[rb] = reinterpret_cast<const unsigned char*>(wq) + (size_t)r1 * RS + (lo ? q : 4 + q) * 16;
+        p2[rb] = reinterpret_cast<const unsigned char*>(wq) + (size_t)r2 * RS + (lo ? 4 + q : q) * 16;
+        rj[rb] = nb + j < N ? nb + j : N - 1;
+    }
     const int jr = j % M, jg = j / M;
     const v4i zero = {0, 0, 0, 0};
 
-    float yacc[M];
+    float yacc[RB][M];
 #pragma unroll
-    for (int r = 0; r < M; r++) yacc[r] = 0.f;
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int r = 0; r < M; r++) yacc[rb][r] = 0.f;
 
     for (int c = c_lo + w; c < c_hi; c += W) {
         const int g0 = uniform(c * GPW);
-        // (1) this wave's scales: 16 rows x GPW fp16, as dwords (even NG: every
-        //     row starts 4-byte aligned) or as halves (odd NG)
-        uint32_t sw[(GPW / 2 + 3) / 4];
+        // (1) this wave's scales: RB x 16 rows x GPW fp16, as dwords (even NG:
+        //     every row starts 4-byte aligned) or as halves (odd NG)
+        uint32_t sw[RB][(GPW / 2 + 3) / 4];
 #pragma unroll
-        for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
-            const int dw = q + 4 * d;
-            const int g = g0 + 2 * dw;
-            const uint16_t* sp = ws + (size_t)rj * NG;
-            uint32_t v = 0;
-            if (dw < GPW / 2 && g < NG) {
-                if (!(NG & 1))
-                    v = *reinterpret_cast<const uint32_t*>(sp + g);
-                else
-                    v = (uint32_t)sp[g] | (g + 1 < NG ? (uint32_t)sp[g + 1] << 16 : 0u);
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
+                const int dw = q + 4 * d;
+                const int g = g0 + 2 * dw;
+                const uint16_t* sp = ws + (size_t)rj[rb] * NG;
+                uint32_t v = 0;
+                if (dw < GPW / 2 && g < NG) {
+                    if (!(NG & 1))
+                        v = *reinterpret_cast<const uint32_t*>(sp + g);
+                    else
+                        v = (uint32_t)sp[g] | (g + 1 < NG ? (uint32_t)sp[g + 1] << 16 : 0u);
+                }
+                sw[rb][d] = v;
             }
-            sw[d] = v;
-        }
         // (2) activations: set s, lane j holds row j%M of group g0 + s*GPS + j/M
         //     (QIN: its fp32 values, quantized after the weight loads are issued)
         uint4 ax0[NSET], ax1[NSET];
@@ -222,20 +237,27 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
         // (3) the weight stream.  A pair starting at the last group of an odd NG
         //     has no second group: its lanes read the first group again (in bounds)
         //     and that result is never used.
-        v4u a[NP], b[NP];
+        v4u a[RB][NP], b[RB][NP];
 #pragma unroll
         for (int p = 0; p < NP; p++) {
             int gp = g0 + 2 * p;
             if (gp >= NG) gp = NG >= 2 ? NG - 2 : 0;
             const int tail = (gp + 1 >= NG) ? 64 : 0;
-            a[p] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p1 + (size_t)gp * 64 - (lo ? 0 : tail)));
-            b[p] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p2 + (size_t)gp * 64 - (lo ? tail : 0)));
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                a[rb][p] = __builtin_nontemporal_load(
+                    reinterpret_cast<const v4u*>(p1[rb] + (size_t)gp * 64 - (lo ? 0 : tail)));
+                b[rb][p] = __builtin_nontemporal_load(
+                    reinterpret_cast<const v4u*>(p2[rb] + (size_t)gp * 64 - (lo ? tail : 0)));
+            }
         }
 #pragma unroll
-        for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
-            const int dw = q + 4 * d;
-            if (dw < GPW / 2) wsl[j * (GPW / 2) + dw] = sw[d];
-        }
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
+                const int dw = q + 4 * d;
+                if (dw < GPW / 2) wsl[(rb * 16 + j) * (GPW / 2) + dw] = sw[rb][d];
+            }
         if constexpr (QIN) {
 #pragma unroll
             for (int s = 0; s < NSET; s++) quant_lane(xv[s], ax0[s], ax1[s], asc[s]);
@@ -243,24 +265,26 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
 
 #pragma unroll
         for (int p = 0; p < NP; p++) {
-            v4u t0, x;
-            t0.x = lo ? a[p].x : b[p].x;
-            t0.y = lo ? a[p].y : b[p].y;
-            t0.z = lo ? a[p].z : b[p].z;
-            t0.w = lo ? a[p].w : b[p].w;
-            x.x = lo ? b[p].x : a[p].x;
-            x.y = lo ? b[p].y : a[p].y;
-            x.z = lo ? b[p].z : a[p].z;
-            x.w = lo ? b[p].w : a[p].w;
-            v4u t1;
-            t1.x = dpp<0x128>(x.x);
-            t1.y = dpp<0x128>(x.y);
-            t1.z = dpp<0x128>(x.z);
-            t1.w = dpp<0x128>(x.w);
+            v4u t0[RB], t1[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                v4u x;
+                t0[rb].x = lo ? a[rb][p].x : b[rb][p].x;
+                t0[rb].y = lo ? a[rb][p].y : b[rb][p].y;
+                t0[rb].z = lo ? a[rb][p].z : b[rb][p].z;
+                t0[rb].w = lo ? a[rb][p].w : b[rb][p].w;
+                x.x = lo ? b[rb][p].x : a[rb][p].x;
+                x.y = lo ? b[rb][p].y : a[rb][p].y;
+                x.z = lo ? b[rb][p].z : a[rb][p].z;
+                x.w = lo ? b[rb][p].w : a[rb][p].w;
+                t1[rb].x = dpp<0x128>(x.x);
+                t1[rb].y = dpp<0x128>(x.y);
+                t1[rb].z = dpp<0x128>(x.z);
+                t1[rb].w = dpp<0x128>(x.w);
+            }
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int u = 2 * p + h, g = g0 + u;
-                const v4u qv = h ? t1 : t0;
                 uint4 xa, xb;
                 switch (u % GPS) {
 #define RT4_PULL(I)                                      \
@@ -275,91 +299,135 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
                 }
                 const v4i A0 = {(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w};
                 const v4i A1 = {(int)xb.x, (int)xb.y, (int)xb.z, (int)xb.w};
-                const v4i b0 = {(int)even_x16(qv.x), (int)odd_x16(qv.x), (int)even_x16(qv.y), (int)odd_x16(qv.y)};
-                const v4i b1 = {(int)even_x16(qv.z), (int)odd_x16(qv.z), (int)even_x16(qv.w), (int)odd_x16(qv.w)};
-                v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, zero, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, acc, 0, 0, 0);
-                // lane l < 16 now holds 16*I[m=r][n0+l] in acc[r]
+                float a_s[M];
                 if (g < NG) {
-                    if (GSUM && lane < 16 && n0 + lane < N)
-#pragma unroll
-                        for (int r = 0; r < M; r++) gsum[((size_t)r * N + n0 + lane) * NG + g] = acc[r] >> 4;
-                    const uint32_t pair = wsl[j * (GPW / 2) + p];
-                    const float s16 = f16_bits_to_f32((uint16_t)(h ? pair >> 16 : pair & 0xFFFFu)) * 0.0625f;
 #pragma unroll
                     for (int r = 0; r < M; r++) {
-                        float a_s;
                         if constexpr (QIN)  // the scale of (row r, group g) sits in lane (u % GPS) * M + r
-                            a_s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(asc[u / GPS]), (u % GPS) * M + r));
+                            a_s[r] = __int_as_float(
+                                __builtin_amdgcn_readlane(__float_as_int(asc[u / GPS]), (u % GPS) * M + r));
                         else
-                            a_s = sa[(size_t)r * NG + g];
-                        yacc[r] = fmaf((float)acc[r], s16 * a_s, yacc[r]);
+                            a_s[r] = sa[(size_t)r * NG + g];
+                    }
+                }
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
+                    const v4u qv = h ? t1[rb] : t0[rb];
+                    const v4i b0 = {(int)even_x16(qv.x), (int)odd_x16(qv.x), (int)even_x16(qv.y), (int)odd_x16(qv.y)};
+                    const v4i b1 = {(int)even_x16(qv.z), (int)odd_x16(qv.z), (int)even_x16(qv.w), (int)odd_x16(qv.w)};
+                    v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, zero, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, acc, 0, 0, 0);
+                    // lane l < 16 now holds 16*I[m=r][n0+16rb+l] in acc[r]
+                    if (g < NG) {
+                        const int nl = n0 + 16 * rb + lane;
+                        if (GSUM && lane < 16 && nl < N)
+#pragma unroll
+                            for (int r = 0; r < M; r++) gsum[((size_t)r * N + nl) * NG + g] = acc[r] >> 4;
+                        const uint32_t pair = wsl[(rb * 16 + j) * (GPW / 2) + p];
+                        const float s16 = f16_bits_to_f32((uint16_t)(h ? pair >> 16 : pair & 0xFFFFu)) * 0.0625f;
+#pragma unroll
+                        for (int r = 0; r < M; r++) yacc[rb][r] = fmaf((float)acc[r], s16 * a_s[r], yacc[rb][r]);
                     }
                 }
             }
         }
     }
 
+    // Outputs of the tile: o = (rb*M + r)*16 + l is row r, column n0 + 16 rb + l.
+    constexpr int NOUT = RB * M * 16;
     if (W == 1 && !piece) {
-        if (lane < 16 && n0 + lane < N)
+        if (lane < 16)
 #pragma unroll
-            for (int r = 0; r < M; r++) y[(size_t)r * N + n0 + lane] = yacc[r];
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int r = 0; r < M; r++)
+                    if (n0 + 16 * rb + lane < N) y[(size_t)r * N + n0 + 16 * rb + lane] = yacc[rb][r];
         return;
     }
     if (lane < 16)
 #pragma unroll
-        for (int r = 0; r < M; r++) red[(w * M + r) * 16 + lane] = yacc[r];
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int r = 0; r < M; r++) red[(w * NOUT) + (rb * M + r) * 16 + lane] = yacc[rb][r];
     __syncthreads();
-    const int cl = threadIdx.x & 15, rr = threadIdx.x >> 4;
-    float tot = 0.f;
-    if (threadIdx.x < M * 16)
-        for (int v = 0; v < W; v++) tot += red[(v * M + rr) * 16 + cl];
+    // each thread sums the waves' partials of outputs o = threadIdx.x + i*blockDim.x
+    constexpr int OPT = (NOUT + 63) / 64;    // outputs per thread at one wave (upper bound)
+    float tot[OPT];
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        tot[i] = 0.f;
+        if (o < NOUT)
+            for (int v = 0; v < W; v++) tot[i] += red[v * NOUT + o];
+    }
     if (!piece) {
-        if (threadIdx.x < M * 16 && n0 + cl < N) y[(size_t)rr * N + n0 + cl] = tot;
+#pragma unroll
+        for (int i = 0; i < OPT; i++) {
+            const int o = threadIdx.x + i * blockDim.x;
+            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
+            if (o < NOUT && n < N) y[(size_t)r * N + n] = tot[i];
+        }
         return;
     }
     // A K range of a split tile: publish the partial (agent-coherent store), count
     // the pieces in, and let the last one sum all pieces in order (deterministic)
     // and reset the counter for the next call.  No workgroup waits for another.
     __shared__ int s_last;
-    if (threadIdx.x < M * 16) store_dev(sp.part + ((size_t)b * M + rr) * 16 + cl, tot);
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        if (o < NOUT) store_dev(sp.part + (size_t)b * NOUT + o, tot[i]);
+    }
     __syncthreads();
     if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(sp.cnt + rem, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sp.S - 1;
     __syncthreads();
     if (!s_last) return;
-    if (threadIdx.x < M * 16) {
-        float sum = 0.f;
-        for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + ((size_t)(rem * sp.S + v) * M + rr) * 16 + cl);
-        if (n0 + cl < N) y[(size_t)rr * N + n0 + cl] = sum;
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        if (o < NOUT) {
+            float sum = 0.f;
+            for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + (size_t)(rem * sp.S + v) * NOUT + o);
+            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
+            if (n < N) y[(size_t)r * N + n] = sum;
+        }
     }
     if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + rem, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int M, int GPW, bool GSUM, bool QIN>
+template <int M, int GPW, int RB, bool GSUM, bool QIN>
 hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                       const float* sa, const float* xf, int N, int K, int waves, const GemvSplit& sp,
                       hipStream_t st) {
-    const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * M * 16 * sizeof(float);
+    const size_t smem = (size_t)waves * 16 * GPW * 2 * RB + (size_t)waves * RB * M * 16 * sizeof(float);
     const int grid = sp.full + sp.nrem * sp.S;
-    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, GSUM, QIN>), dim3(grid), dim3(64 * waves), smem, st, wq, ws, xq, sa,
-                       xf, y, gsum, N, K, sp);
+    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, GSUM, QIN>), dim3(grid), dim3(64 * waves), smem, st, wq, ws, xq,
+                       sa, xf, y, gsum, N, K, sp);
     return hipGetLastError();
+}
+
+template <int M, int RB, bool GSUM, bool QIN>
+hipError_t launch_g(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                    const float* sa, const float* xf, int N, int K, const GemvCfg& c, const GemvSplit& sp,
+                    hipStream_t st) {
+    switch (c.gpw) {
+        case 2: return launch_one<M, 2, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 4: return launch_one<M, 4, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 6: return launch_one<M, 6, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 8: return launch_one<M, 8, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 10: return launch_one<M, 10, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+        case 12: return launch_one<M, 12, RB, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 template <int M, bool GSUM, bool QIN>
 hipError_t launch_m(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                     const float* sa, const float* xf, int N, int K, const GemvCfg& c, const GemvSplit& sp,
                     hipStream_t st) {
-    switch (c.gpw) {
-        case 2: return launch_one<M, 2, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-        case 4: return launch_one<M, 4, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-        case 6: return launch_one<M, 6, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-        case 8: return launch_one<M, 8, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-        case 10: return launch_one<M, 10, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-        case 12: return launch_one<M, 12, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c.waves, sp, st);
-    }
-    return hipErrorInvalidValue;
+    return c.rb == 2 ? launch_g<M, 2, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st)
+                     : launch_g<M, 1, GSUM, QIN>(y, gsum, wq, ws, xq, sa, xf, N, K, c, sp, st);
 }
 
 template <bool GSUM, bool QIN>
@@ -377,8 +445,7 @@ hipError_t launch_rows(float* y, int32_t* gsum, const uint32_t* wq, const uint16
 
 }  // namespace
 
-GemvCfg gemv_default_cfg(int rows, int N, int K) {
-    (void)N;
+GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
     const int NG = K / kGroup;
     GemvCfg c;
     // Measured on MI355X over the 27B shapes (K = 5120 and 17408, N = 5120 and
@@ -395,6 +462,14 @@ GemvCfg gemv_default_cfg(int rows, int N, int K) {
     w = w < nc ? w : nc;
     c.waves = w < kGemvMaxWaves ? w : kGemvMaxWaves;
     c.max_split = 0;
+    // Two 16-row blocks per tile when each CU has enough tile x group work for
+    // the last round's imbalance not to matter, and the activation operand is
+    // wide enough for its reuse to pay (3-4 rows).  Measured at 4 rows: LM head
+    // (N = 248320) 114 vs 128 us; K = 17408, N = 40960 68 vs 78 us; below about
+    // 300 (32-row tile x group) units per CU it is slower (N = 17408 at K =
+    // 5120: 13.6 vs 12.7 us).  One row: slower at every N.
+    cus = cus > 0 ? cus : 256;
+    c.rb = rows >= kGemvRb2MinRows && (long long)((N + 31) / 32) * NG >= (long long)kGemvRb2Work * cus ? 2 : 1;
     return c;
 }
 
@@ -402,18 +477,19 @@ bool gemv_cfg_valid(const GemvCfg& c, int K) {
     const int NG = K / kGroup;
     if (c.gpw < 2 || c.gpw > 12 || (c.gpw & 1)) return false;
     const int nc = (NG + c.gpw - 1) / c.gpw;
-    return c.waves >= 1 && c.waves <= kGemvMaxWaves && c.waves <= nc && c.max_split >= 0 && c.max_split <= 64;
+    return c.waves >= 1 && c.waves <= kGemvMaxWaves && c.waves <= nc && c.max_split >= 0 && c.max_split <= 64 &&
+           (c.rb == 1 || c.rb == 2);
 }
 
 GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus) {
-    // Whole 16-row tiles in a multiple of the CU count; the remaining tiles are
+    // Whole tiles (16*rb rows) in a multiple of the CU count; the remaining tiles are
     // cut along K into S pieces, about one piece per CU, so every CU streams the
     // same number of weight bytes (a round of whole tiles with a few tiles left
     // over would otherwise run at a fraction of the machine).  The combine costs a
     // round trip through L2, which only pays for deep K: by default a piece keeps
     // at least 32 groups (K = 17408 gains ~25%, K = 5120 loses ~5% when split).
     GemvSplit sp{};
-    const int ntiles = (N + 15) / 16;
+    const int ntiles = (N + 16 * c.rb - 1) / (16 * c.rb);
     const int NC = (K / kGroup + c.gpw - 1) / c.gpw;
     cus = cus > 0 ? cus : 256;
     sp.full = ntiles / cus * cus;
@@ -433,8 +509,8 @@ GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus) {
     return sp;
 }
 
-size_t gemv_part_bytes(const GemvSplit& sp, int rows) {
-    return (size_t)sp.nrem * sp.S * rows * 16 * sizeof(float);
+size_t gemv_part_bytes(const GemvSplit& sp, int rows, int rb) {
+    return (size_t)sp.nrem * sp.S * rb * rows * 16 * sizeof(float);
 }
 
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,

@@ -28,23 +28,27 @@ hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG
 // ---- decode GEMV (gemv.hip)
 struct GemvCfg {
     int gpw;    // K groups per wave (even, 2..12)
-    int waves;  // waves per workgroup; they share one 16-row tile and split its K groups
+    int waves;  // waves per workgroup; they share one tile and split its K groups
     int max_split;  // leftover tiles are cut along K into at most this many pieces (1: never,
                     // 0: as many as keep 32 groups per piece)
+    int rb;     // 16-row blocks per tile (1 or 2): a wave applies its activations to rb blocks
 };
 constexpr int kGemvMaxWaves = 16;
-GemvCfg gemv_default_cfg(int rows, int N, int K);
+constexpr int kGemvMaxRb = 2;
+constexpr int kGemvRb2MinRows = 3;     // default rb = 2 needs this many activation rows
+constexpr int kGemvRb2Work = 320;      // and this many (32-row tile x K group) units per CU
+GemvCfg gemv_default_cfg(int rows, int N, int K, int cus);
 bool gemv_cfg_valid(const GemvCfg& c, int K);
-// Grid of the GEMV: `full` whole 16-row tiles, then `nrem` tiles cut along K into
-// S pieces each, whose partials (part: nrem*S*rows*16 floats) are summed by the
-// last piece to arrive (cnt: nrem counters, zero between calls).
+// Grid of the GEMV: `full` whole tiles of 16*rb rows, then `nrem` tiles cut along
+// K into S pieces each, whose partials (part: nrem*S*rb*rows*16 floats) are summed
+// by the last piece to arrive (cnt: nrem counters, zero between calls).
 struct GemvSplit {
     int full, nrem, S;
     float* part;
     int* cnt;
 };
 GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus);
-size_t gemv_part_bytes(const GemvSplit& sp, int rows);
+size_t gemv_part_bytes(const GemvSplit& sp, int rows, int rb);
 // Activations either pre-quantized (xq, sa; xf null) or fp32 xf [rows][K], 16-byte
 // aligned, quantized inside the kernel exactly as launch_quant_act_a8 would.
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,

@@ -68,11 +68,11 @@ _SIGS = {
     "rt4_gemv_w4a4": [_P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemm_w4a4": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
-    "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
-    "rt4_gemv_launch_plan": [_I, _I, _I, _P, _P, _P],
+    "rt4_gemv_w4a8_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_gemv_launch_plan": [_I, _I, _I, _P, _P, _P, _P],
     "rt4_gemv_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8": [_P, _P, _P, _P, _I, _I, _I, _P],
-    "rt4_gemv_w4a8_cfg": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_cfg": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_a8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_i8": [_P, _P, _P, _I, _I, _I, _I, _P],
     "rt4_digits_to_i8": [_P, _P, _P, _I, _I, _P],
@@ -161,25 +161,28 @@ def quant_act_a8(x, want_sums: bool = False):
     return (xq, sa, asu) if want_sums else (xq, sa)
 
 
-def gemv_w4a8_q(wq, ws, xq, sa, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0):
+def gemv_w4a8_q(wq, ws, xq, sa, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0,
+                row_blocks: int = 0):
     """W4A8 GEMV on quantized activations.  wq int32/uint32 [N, K/8], ws int16/fp16 [N, K/128].
 
-    groups_per_wave / waves / k_splits override the launch configuration (0 keeps
-    the default; k_splits=1 keeps every 16-row tile whole)."""
+    groups_per_wave / waves / k_splits / row_blocks override the launch
+    configuration (0 keeps the default; k_splits=1 keeps every tile whole;
+    row_blocks 1 or 2 sixteen-row blocks per tile)."""
     torch = _torch()
     rows, K = xq.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, xq.device)
     _check(lib().rt4_gemv_w4a8_q_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(xq), _ptr(sa), rows, N, K,
-                                     groups_per_wave, waves, k_splits, _stream()))
+                                     groups_per_wave, waves, k_splits, row_blocks, _stream()))
     return y
 
 
 def gemv_launch_plan(rows: int, N: int, K: int) -> dict:
     """The default GEMV launch configuration for this shape on the current device."""
-    g, w, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _check(lib().rt4_gemv_launch_plan(rows, N, K, ctypes.byref(g), ctypes.byref(w), ctypes.byref(s)))
-    return {"groups_per_wave": g.value, "waves": w.value, "k_splits": s.value}
+    g, w, s, r = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(lib().rt4_gemv_launch_plan(rows, N, K, ctypes.byref(g), ctypes.byref(w), ctypes.byref(s),
+                                      ctypes.byref(r)))
+    return {"groups_per_wave": g.value, "waves": w.value, "k_splits": s.value, "row_blocks": r.value}
 
 
 def gemv_w4a8_groupsums(wq, ws, xq, sa):
@@ -194,7 +197,8 @@ def gemv_w4a8_groupsums(wq, ws, xq, sa):
     return y, gs
 
 
-def gemv_w4a8(wq, ws, x, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0):
+def gemv_w4a8(wq, ws, x, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0,
+              row_blocks: int = 0):
     """Drop-in k_gemv_w4a8: quantize x f32 [rows, K] and multiply (rows <= 4).
 
     Two launches (quantizer, GEMV).  A launch configuration (see gemv_w4a8_q)
@@ -204,9 +208,9 @@ def gemv_w4a8(wq, ws, x, out=None, groups_per_wave: int = 0, waves: int = 0, k_s
     rows, K = x.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, x.device)
-    if groups_per_wave or waves or k_splits:
+    if groups_per_wave or waves or k_splits or row_blocks:
         _check(lib().rt4_gemv_w4a8_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, groups_per_wave, waves,
-                                       k_splits, _stream()))
+                                       k_splits, row_blocks, _stream()))
     else:
         _check(lib().rt4_gemv_w4a8(_ptr(y), _ptr(wq), _ptr(ws), _ptr(x), rows, N, K, _stream()))
     return y

@@ -59,10 +59,11 @@ def test_gemv_shape_errors(rt4, rows, N, K):
 def test_gemv_null_and_config_errors(rt4):
     L = rt4.lib()
     assert L.rt4_gemv_w4a8(None, DUMMY, DUMMY, DUMMY, 1, 64, 256, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 1, 0, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 2, 0, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 14, 1, 0, None) == 2
-    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 65, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 1, 0, 0, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 2, 0, 0, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 14, 1, 0, 0, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 65, 0, None) == 2
+    assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 0, 3, None) == 2
     assert "config" in L.rt4_last_error().decode()
 
 

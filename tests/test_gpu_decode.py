@@ -62,9 +62,9 @@ def _gemv_inputs(torch, seed, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (2, 40, 512), (3, 96, 1024), (4, 200, 2048),
                                    (4, 17, 128), (4, 1024, 5120), (3, 33, 384), (2, 48, 1920),
-                                   (4, 64, 40960), (1, 16, 128)])
+                                   (4, 64, 40960), (1, 16, 128), (3, 65560, 384), (4, 70000, 256)])
 def test_gemv_groupsums_bit_exact(rt4, orc, torch_gpu, M, N, K):
-    print(f"case gemv_groupsums M={M} N={N} K={K}", flush=True)
+    print(f"case gemv_groupsums M={M} N={N} K={K} plan={rt4.gemv_launch_plan(M, N, K)}", flush=True)
     c, wq, ws, x = _gemv_inputs(torch_gpu, 7, M, N, K)
     xq, sa = rt4.quant_act_a8(x)
     y, gs = rt4.gemv_w4a8_groupsums(wq, ws, xq, sa)
@@ -74,6 +74,40 @@ def test_gemv_groupsums_bit_exact(rt4, orc, torch_gpu, M, N, K):
     assert np.array_equal(host(gs), I)
     ref = orc.gemv_fold(I, c["ws"], sa_o)
     assert rel_l2(host(y), ref) < TIGHT
+
+
+def test_gemv_default_row_blocks(rt4, torch_gpu):
+    """Two 16-row blocks per tile only for 3-4 activation rows and where each CU
+    has at least 320 (32-row tile x K group) units: the LM head, not the 27B MLP
+    shapes."""
+    cus = torch_gpu.cuda.get_device_properties(0).multi_processor_count
+    for M, N, K in [(4, 17408, 5120), (4, 5120, 17408), (4, 248320, 5120), (1, 248320, 5120),
+                    (3, 40960, 17408), (2, 248320, 5120)]:
+        want = 2 if M >= 3 and (N + 31) // 32 * (K // 128) >= 320 * cus else 1
+        assert rt4.gemv_launch_plan(M, N, K)["row_blocks"] == want, (M, N, K, cus)
+
+
+@pytest.mark.parametrize("M,N,K,gpw,waves", [(4, 300, 3072, 4, 6), (1, 17, 128, 2, 1), (2, 40, 512, 4, 1),
+                                             (3, 1000, 5120, 4, 8), (4, 4176, 8192, 4, 8), (1, 520, 2944, 10, 2),
+                                             (4, 64, 40960, 8, 16), (2, 48, 1920, 12, 1), (4, 33, 1408, 6, 2)])
+def test_gemv_row_blocks(rt4, orc, torch_gpu, M, N, K, gpw, waves):
+    """Tiles of two 16-row blocks: whole tiles give y bit-identical to one block
+    per tile (same per-lane and per-wave sum order); with leftover tiles cut along
+    K the result stays within the bar of the oracle and repeats exactly."""
+    print(f"case gemv_rb M={M} N={N} K={K} gpw={gpw} waves={waves}", flush=True)
+    c, wq, ws, x = _gemv_inputs(torch_gpu, 12, M, N, K)
+    xq, sa = rt4.quant_act_a8(x)
+    kw = dict(groups_per_wave=gpw, waves=waves)
+    y1 = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=1, row_blocks=1, **kw)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=1, row_blocks=2, **kw)
+    ys = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=64, row_blocks=2, **kw)
+    ys2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, k_splits=64, row_blocks=2, **kw)
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
+    ref = orc.gemv_w4a8(c["wq"], c["ws"], c["x"])
+    assert rel_l2(host(y2), ref) < TIGHT
+    assert rel_l2(host(ys), ref) < TIGHT
+    assert np.array_equal(host(ys), host(ys2))
 
 
 @pytest.mark.parametrize("gpw,waves", [(2, 1), (2, 12), (4, 3), (4, 6), (6, 4), (8, 2), (10, 3), (12, 1),
@@ -128,9 +162,11 @@ def fused_edge_acts(rng, M, K):
 
 
 @pytest.mark.parametrize("M,N,K,cfg", [(1, 5120, 5120, None), (2, 1000, 5120, None), (3, 2064, 17408, None),
-                                       (4, 17408, 5120, None), (4, 5120, 17408, None), (4, 300, 3072, (2, 12, 1)),
-                                       (4, 300, 3072, (6, 4, 3)), (1, 520, 2944, (10, 2, 0)), (2, 64, 40960, (8, 16, 8)),
-                                       (3, 96, 1920, (12, 1, 1))])
+                                       (4, 17408, 5120, None), (4, 5120, 17408, None), (4, 300, 3072, (2, 12, 1, 0)),
+                                       (4, 300, 3072, (6, 4, 3, 0)), (1, 520, 2944, (10, 2, 0, 0)),
+                                       (2, 64, 40960, (8, 16, 8, 0)), (3, 96, 1920, (12, 1, 1, 0)),
+                                       (4, 300, 3072, (4, 6, 1, 2)), (4, 1000, 5120, (4, 8, 0, 2)),
+                                       (1, 520, 2944, (10, 2, 4, 2))])
 def test_gemv_fused_quant_equals_two_launches(rt4, orc, torch_gpu, M, N, K, cfg):
     """The one-launch linear (activations quantized in the GEMV's registers) against
     rt4_quant_act_a8 + the GEMV on the same config: outputs identical bit for bit
@@ -140,10 +176,10 @@ def test_gemv_fused_quant_equals_two_launches(rt4, orc, torch_gpu, M, N, K, cfg)
     c = workload.gemv_case(N=N, K=K, M=M, seed=int(rng.integers(1 << 30)))
     x_np = fused_edge_acts(rng, M, K)
     wq, ws, x = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["ws"]), dev(torch_gpu, x_np)
-    g, w, s = cfg or (0, 0, 0)
-    y = rt4.gemv_w4a8(wq, ws, x, groups_per_wave=g, waves=w, k_splits=s)
+    g, w, s, rb = cfg or (0, 0, 0, 0)
+    y = rt4.gemv_w4a8(wq, ws, x, groups_per_wave=g, waves=w, k_splits=s, row_blocks=rb)
     xq, sa = rt4.quant_act_a8(x)
-    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=g, waves=w, k_splits=s)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=g, waves=w, k_splits=s, row_blocks=rb)
     torch_gpu.cuda.synchronize()
     assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
     if N * K <= 5120 * 5120:
