@@ -34,6 +34,8 @@
 // issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.
+#include <type_traits>
+
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -273,7 +275,10 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         S.ks = ksc[(size_t)((tid >> 6) & 1) * kv_cap + (tid < 2 * BNK && j < kv_cap ? j : 0)];
         S.vs = vsc[(size_t)(t < kv_cap / BNK ? t : 0) * HD + tid];
     };
-    auto store = [&](const Stage& S, int b, int t) {
+    // WHOLE: the tile lies wholly below n_kv and needs none of the zero
+    // substitutions (the caller picks the instance with a uniform branch).
+    auto store = [&](const Stage& S, int b, int t, auto whole_tag) {
+        constexpr bool whole = decltype(whole_tag)::value;
         const int kb = t * BNK;
         unsigned char* kub = ku + b * KU_BYTES;
         unsigned char* vub = vu + b * VU_BYTES;
@@ -282,8 +287,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             const int kk = tid & 63, p = tid >> 6;
             const bool kin = kb + kk < n_kv;
             uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
+            if constexpr (!whole)
 #pragma unroll
-            for (int g = 0; g < 8; g++) d[g] = kin ? d[g] : 0u;
+                for (int g = 0; g < 8; g++) d[g] = kin ? d[g] : 0u;
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
@@ -293,12 +299,16 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         }
         {   // V: lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3
             // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
-            uint32_t e[8], o[8];
+            uint32_t e[8], o[8], vv[8];
+#pragma unroll
+            for (int g = 0; g < 8; g++) vv[g] = S.v[g];
+            if constexpr (!whole)
+#pragma unroll
+                for (int g = 0; g < 8; g++) vv[g] = (kb / 8 + g) * 8 + 8 <= n_kv ? vv[g] : 0u;
 #pragma unroll
             for (int g = 0; g < 8; g++) {
-                const uint32_t v = (kb / 8 + g) * 8 + 8 <= n_kv ? S.v[g] : 0u;
-                e[g] = even_x16(v);
-                o[g] = odd_x16(v);
+                e[g] = even_x16(vv[g]);
+                o[g] = odd_x16(vv[g]);
             }
 #pragma unroll
             for (int g = 0; g < 4; g++) {
@@ -313,6 +323,10 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         }
         if (tid < 2 * BNK) ks_l[b][tid] = kb + (tid & 63) < kv_cap ? S.ks : 1.f;
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
+    };
+    auto store_tile = [&](const Stage& S, int b, int t) {
+        if ((t + 1) * BNK <= n_kv) store(S, b, t, std::true_type{});
+        else store(S, b, t, std::false_type{});
     };
 
     const v4i zero = {0, 0, 0, 0};
@@ -358,8 +372,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // only after a visible tile; -inf gives the same P there and also keeps a row
         // that has seen nothing yet -- possible at the start of a KV split -- at zero.)
         if (m < -1e29f) m = rref;
-        // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand
-        int isum = 0;
+        // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand.
+        // The clamp of the reference never binds here: m is the max of the row's S
+        // (fmaxf returns one of its operands), so S - m <= 0, 2^(S - m) is in [0, 1]
+        // (v_exp_f32 is within 1 ulp, and no value up to 8/7 could reach P = 8),
+        // and the truncation of 7*2^(S - m) + 0.5 lies in [0, 7]; a fully masked row
+        // has m = rref, S - m = -inf and P = 0.
         uint32_t pk[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
@@ -369,15 +387,15 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 // v_exp_f32 directly: the arguments are <= 0 and any result below
                 // 2^-4 quantizes to P = 0, so denormal handling is irrelevant here
                 const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m) * 7.f;
-                int q = (int)(p + 0.5f);
-                q = q > 7 ? 7 : (q < 0 ? 0 : q);
-                pq[r] = q;
-                isum += q;
+                pq[r] = (int)(p + 0.5f);
             }
             pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[2] << 8 | (uint32_t)pq[1] << 16 | (uint32_t)pq[3] << 24;
         }
-        isum += __shfl_xor(isum, 16);
-        isum += __shfl_xor(isum, 32);
+        const v4i pop = {(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        // Σ_k P of the row over the tile's 64 keys on the matrix pipe: an A operand
+        // of ones gives it in every output row (exact integers)
+        const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+        const int isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, pop, zero, 0, 0, 0)[0];
         const float r_new = fmaxf(rref, m);
         const float alpha = exp2f(rref - r_new);
         const float beta = exp2f(m - r_new);
@@ -385,7 +403,6 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         L = L * alpha + (float)isum * (beta / 7.f);
         rref = r_new;
         // ---- O^T = V^T P^T, folded per dim tile
-        const v4i pop = {(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
         const float pb16 = pb * 0.0625f;          // V is x16 unpacked
         // O * alpha is exact when alpha == 1 (running max unchanged): skip it when
         // that holds for every row of the wave (a wave-uniform branch)
@@ -409,7 +426,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     Stage S;
     if (t0 < t1) {
         load(S, t0);
-        store(S, t0 & 1, t0);
+        store_tile(S, t0 & 1, t0);
         if (t0 + 1 < t1) load(S, t0 + 1);
     }
     __syncthreads();
@@ -419,7 +436,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // compute tile t.  Storing before computing keeps S's registers free during
         // the compute phase.
         if (t + 1 < t1) {
-            store(S, (t + 1) & 1, t + 1);
+            store_tile(S, (t + 1) & 1, t + 1);
             if (t + 2 < t1) load(S, t + 2);
         }
         // keep the loads here: left to itself the compiler sinks them next to their
