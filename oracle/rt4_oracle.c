@@ -601,7 +601,13 @@ static double fa_v(const uint32_t* V, const float* Vs, int j, int d) {
  * mode 1: the kernel's fixed-point algorithm in fp64, restating ref_alg
  *         (kernels/flash_attn_int4.hip:175-217): per 64-key tile the row max mt,
  *         P = round(7 exp(s - mt)) in [0, 7], online rescale alpha = exp(r_old - r_new),
- *         beta = exp(mt - r_new) / 7, out = O / L.
+ *         beta = exp(mt - r_new) / 7, out = O / L.  For n_kv that is not a
+ *         multiple of 64, where ref_alg (whole tiles only) is not defined, the
+ *         reference kernel's loads decide (kernels/flash_attn_core.h:143-152): the
+ *         partial last tile is processed, and V is read per whole 8-key group only,
+ *         so the keys of a partial group (n_kv % 8 != 0) count in P and L with a V
+ *         of zero.  (K past n_kv reads as zero codes there too; causality already
+ *         hides those keys.)
  * out f64 [nrows][256]. */
 void rt4o_fa_rows(const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                   const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int kv_cap, int ratio,
@@ -650,9 +656,10 @@ void rt4o_fa_rows(const uint32_t* qq, const float* qsc, const uint32_t* kc, cons
                 }
                 const double r_new = r_old > mt ? r_old : mt;
                 const double alpha = exp(r_old - r_new), beta = exp(mt - r_new) / 7.0;
+                const int jv = (n_kv / 8) * 8;   /* keys j >= jv: partial 8-group, V read as zero */
                 for (int d = 0; d < RT4O_HD; d++) {
                     double acc = 0.0;
-                    for (int j = j0; j <= j1; j++) acc += p[j - j0] * fa_v(V, Vs, j, d);
+                    for (int j = j0; j <= j1 && j < jv; j++) acc += p[j - j0] * fa_v(V, Vs, j, d);
                     O[d] = O[d] * alpha + beta * acc;
                 }
                 L = L * alpha + beta * psum;

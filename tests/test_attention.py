@@ -144,7 +144,11 @@ def test_exact_softmax_oracle_matches_numpy(orc):
 
 
 def np_tile_algorithm(Q, K, V, rows, off, n_kv):
-    """The fixed-point online softmax of fa_int4, written out in numpy (fp64)."""
+    """The fixed-point online softmax of fa_int4, written out in numpy (fp64).  V is
+    read per whole 8-key group, as the reference kernel loads it
+    (kernels/flash_attn_core.h:150-152): keys of a partial last group get V = 0."""
+    V = V.copy()
+    V[n_kv // 8 * 8:] = 0.0
     out = []
     for i in rows:
         pos = min(off + i, n_kv - 1)
@@ -173,6 +177,32 @@ def test_algorithm_oracle_matches_numpy_restatement(orc):
         got = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, off, n_kv, ratio, 1, rows, 1)
         Q, K, V = dequant(qq, qs, kc, ksc, vc, vsc, 1, ratio)
         assert rel_l2(got, np_tile_algorithm(Q, K, V, rows, off, n_kv)) < 1e-12
+
+
+def test_algorithm_ragged_kv_follows_the_kernel_loads(orc):
+    """n_kv not a multiple of 8 (nor of 64): the tile algorithm matches the numpy
+    restatement with the reference kernel's load rule, and the V codes of the
+    partial 8-key group do not reach the output (planted: set them to the extreme
+    code) while their probabilities still count in L."""
+    for n_kv in (300, 197, 64 * 4 + 3):
+        q, k, v = small_case(seed=8, n_kv=n_kv, scale=True)
+        n_q, ratio = 64, 2
+        cap = (n_kv + BN - 1) // BN * BN
+        qq, qs, kc, ksc, vc, vsc, _ = build_cache(orc, q, k, v, n_q, cap)
+        off = n_kv - n_q
+        rows = np.arange(n_q, dtype=np.int32)
+        got = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, off, cap, ratio, 1, rows, 1)
+        Q, K, V = dequant(qq, qs, kc, ksc, vc, vsc, 1, ratio)
+        assert rel_l2(got, np_tile_algorithm(Q, K, V[:n_kv], rows, off, n_kv)) < 1e-12
+        vc2 = vc.copy()
+        g = n_kv // 8
+        vc2[:, g] = 0x77777777                               # partial group: codes 7 everywhere
+        got2 = orc.fa_rows(qq, qs, kc, ksc, vc2, vsc, n_q, n_kv, off, cap, ratio, 1, rows, 1)
+        assert np.array_equal(got, got2)
+        # the exact softmax does read those keys' V
+        e1 = orc.fa_rows(qq, qs, kc, ksc, vc, vsc, n_q, n_kv, off, cap, ratio, 1, rows, 0)
+        e2 = orc.fa_rows(qq, qs, kc, ksc, vc2, vsc, n_q, n_kv, off, cap, ratio, 1, rows, 0)
+        assert not np.array_equal(e1, e2)
 
 
 def test_algorithm_is_exact_when_scores_are_equal(orc):
@@ -331,6 +361,8 @@ def check_attention(rt4, orc, torch, q, k, v, ratio, off, n_kv, kv_cap, rows_per
     (128, 200, 72, 4, 2, 256, True),       # n_kv not a multiple of 64, kv_cap > n_kv
     (192, 1000, 808, 6, 1, 1024, True),    # ratio 6, partial last tile
     (64, 2048, 1984, 1, 1, 4096, False),   # no GQA, long-ish
+    (128, 300, 172, 6, 2, 320, True),      # GQA ratio 3 over two KV heads; n_kv % 8 != 0: partial V group
+    (64, 520, 456, 8, 2, 576, True),       # ratio 4 over two KV heads
 ])
 def test_attention_against_oracle(rt4, orc, torch_gpu, T, n_kv, off, H, KVH, cap, scale):
     print(f"case attention T={T} n_kv={n_kv} off={off} H={H} KVH={KVH} cap={cap}", flush=True)
