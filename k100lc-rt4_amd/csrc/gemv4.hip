@@ -18,6 +18,12 @@
 // once at the end.  Every per-term product equals the reference's
 // (ws*sa)*I bit for bit (the 1/256 is an exact power of two); only the order of
 // the sums differs.
+//
+// Activation codes and scales of a chunk (M rows x GPW groups) arrive with one
+// whole-wave load each -- per-group loads with 16 active lanes cost ~3 us at the
+// 27B gate/up shape -- and are redistributed through a wave-private LDS slice:
+// codes [row][group][subgroup] in 16-byte slots plus a zero slot that the lanes
+// off the block diagonal read, scales [row][group][subgroup] as floats.
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -32,12 +38,15 @@ __device__ __forceinline__ uint32_t dpp4(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
 
+constexpr int kA4Slots = 4 * 4 * 4;    // 16-byte code slots per wave: [row][group][subgroup], M, GPW <= 4
+
 template <int M, int GPW>
 __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
                                                     const uint32_t* __restrict__ aq,
                                                     const float* __restrict__ sa,
                                                     float* __restrict__ y, int N, int K) {
+    static_assert(GPW == 4, "the chunk's activations are one 16-byte slot per lane");
     constexpr int NP = GPW / 2;                  // group pairs per wave
     extern __shared__ __align__(16) unsigned char smem[];
     const int W = blockDim.x >> 6;
@@ -46,8 +55,18 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
     const int NG = K >> 7, RS = K >> 1, KD = K >> 3, NS = K >> 5;
     const int NC = (NG + GPW - 1) / GPW;
     const int n0 = blockIdx.x * 16;
-    uint32_t* wsl = reinterpret_cast<uint32_t*>(smem) + (size_t)w * 8 * GPW;   // [16 rows][GPW/2] dwords
-    float* red = reinterpret_cast<float*>(smem + (size_t)W * 16 * GPW * 2);    // [W][M][16]
+    // LDS: [W] weight-scale slices ([16 rows][GPW/2] dwords), [W] code slices
+    // (kA4Slots + 1 zero slot, 16 B each), [W] scale slices (kA4Slots floats), then
+    // the reduction area [W][M][16]
+    unsigned char* base = smem;
+    uint32_t* wsl = reinterpret_cast<uint32_t*>(base) + (size_t)w * 8 * GPW;
+    base += (size_t)W * 16 * GPW * 2;
+    uint4* acl = reinterpret_cast<uint4*>(base) + (size_t)w * (kA4Slots + 1);
+    base += (size_t)W * (kA4Slots + 1) * 16;
+    float* asl = reinterpret_cast<float*>(base) + (size_t)w * kA4Slots;
+    base += (size_t)W * kA4Slots * sizeof(float);
+    float* red = reinterpret_cast<float*>(base);
+    if (lane == 0) acl[kA4Slots] = make_uint4(0, 0, 0, 0);
 
     // weight loads: the mapping of the W4A8 GEMV (two instructions per group
     // pair, 8 rows x 128 B each; the first group of the pair is sel(j<8 ? inst1 :
@@ -59,12 +78,17 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
     const unsigned char* p1 = reinterpret_cast<const unsigned char*>(wq) + (size_t)r1 * RS + (lo ? q : 4 + q) * 16;
     const unsigned char* p2 = reinterpret_cast<const unsigned char*>(wq) + (size_t)r2 * RS + (lo ? 4 + q : q) * 16;
     const int rj = n0 + j < N ? n0 + j : N - 1;
-    // activation operand of this lane: row am of subgroup q, used iff j/4 == q
+    // activation operand of this lane: row am of subgroup q, used iff j/4 == q;
+    // for group u it is slot (am*4 + u)*4 + q, the zero slot off the diagonal
     const int am = j & 3;
     const bool aon = (j >> 2) == q && am < M;
-    const int amc = am < M ? am : M - 1;
-    const uint32_t* arow = aq + (size_t)amc * KD + 4 * q;    // + 16 g: subgroup q of group g
-    const float* srow = sa + (size_t)amc * NS + q;            // + 4 g
+    // the chunk's load: lane l < 16M takes row l/16, group (l/4)%4, subgroup l%4
+    const int lr = lane >> 4, lu = (lane >> 2) & 3, ls = lane & 3;
+    const bool lon = lane < 16 * M;
+    const uint32_t* lrow = aq + (size_t)(lon ? lr : 0) * KD + 4 * ls;   // + 16 g
+    const float* lsrow = sa + (size_t)(lon ? lr : 0) * NS + ls;         // + 4 g
+    // this lane's scale in the fold layout (lane 16G + r: row r, subgroup G)
+    const int sslot = j < M ? (j * 4) * 4 + q : -1;                      // + 4 u
     const v4i zero = {0, 0, 0, 0};
 
     float yacc[M];
@@ -90,16 +114,16 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
             }
             sw[d] = v;
         }
-        // (2) activation codes and scales of this lane's (row, subgroup) per group;
-        //     lanes off the diagonal load nothing
-        uint4 av[GPW];
-        float as[GPW];
-#pragma unroll
-        for (int u = 0; u < GPW; u++) {
-            int g = g0 + u;
+        // (2) activation codes and scales of the chunk: one slot / one float per lane
+        uint4 lcode = make_uint4(0, 0, 0, 0);
+        float lscale = 0.f;
+        {
+            int g = g0 + lu;
             g = g < NG ? g : NG - 1;
-            av[u] = aon ? *reinterpret_cast<const uint4*>(arow + 16 * g) : make_uint4(0, 0, 0, 0);
-            as[u] = j < M ? srow[4 * g] : 0.f;
+            if (lon) {
+                lcode = *reinterpret_cast<const uint4*>(lrow + 16 * g);
+                lscale = lsrow[4 * g];
+            }
         }
         // (3) the weight stream
         v4u a[NP], b[NP];
@@ -115,6 +139,20 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
         for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
             const int dw = q + 4 * d;
             if (dw < GPW / 2) wsl[j * (GPW / 2) + dw] = sw[d];
+        }
+        // redistribute the chunk's activations (wave-private slices: the LDS
+        // operations of one wave complete in order, no barrier)
+        if (lon) {
+            acl[lane] = lcode;
+            asl[lane] = lscale;
+        }
+        uint4 av[GPW];
+        float as[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; u++) {
+            av[u] = acl[aon ? (am * 4 + u) * 4 + q : kA4Slots];
+            const float sv = asl[(sslot >= 0 ? sslot : 0) + 4 * u];
+            as[u] = sslot >= 0 ? sv : 0.f;
         }
 
 #pragma unroll
@@ -186,7 +224,8 @@ hipError_t launch_m4(float* y, const uint32_t* wq, const uint16_t* ws, const uin
     constexpr int GPW = 4;
     const int NG = K / 128, NC = (NG + GPW - 1) / GPW;
     const int waves = NC < 8 ? NC : 8;
-    const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * M * 16 * sizeof(float);
+    const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * (kA4Slots + 1) * 16 +
+                        (size_t)waves * kA4Slots * sizeof(float) + (size_t)waves * M * 16 * sizeof(float);
     hipLaunchKernelGGL((gemv_w4a4_k<M, GPW>), dim3((N + 15) / 16), dim3(64 * waves), smem, st, wq, ws, aq, sa, y, N,
                        K);
     return hipGetLastError();
