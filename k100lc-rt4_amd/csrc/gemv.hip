@@ -26,9 +26,17 @@
 //   the activation rows (rows M..15 of A are don't-care; their outputs are
 //   dropped).  Two MFMAs per group; the int32 accumulator holds 16*I exactly
 //   (the x16 nibble unpack, rt4_dev.h).
-// * Activations: loaded straight into registers, 16/M groups per register set
-//   (lane j holds row j%M of group j/M), and rotated into lanes 0..M-1 for the
-//   group being multiplied with DPP row_ror.
+// * Activations: 16/M groups per register set (lane j holds row j%M of group
+//   j/M), rotated into lanes 0..M-1 for the group being multiplied with DPP
+//   row_ror.  With AL (one 16-row block per tile, pre-quantized activations) a
+//   wave's chunk of activations (M rows x GPW groups x 128 B) arrives in whole
+//   cache lines, 16 consecutive bytes per lane, and is redistributed into that
+//   register layout through a wave-private LDS slice (XOR-swizzled so the 16
+//   lanes of a quarter wave hit 16 distinct bank groups); the per-lane form
+//   touches 16 half-used lines per instruction and measured ~5% slower.  The
+//   loads sit in a block of their own so that the compiler keeps them ahead of
+//   the weight stream (sunk behind it, the first MFMA would wait for every
+//   weight load as well).
 // * Weight scales: each wave loads its 16 rows x GPW fp16 scales as dwords into
 //   a private LDS slice.  Scales and activations are issued before the weight
 //   stream: vmcnt retires in order, so the first group can start as soon as its
@@ -134,7 +142,11 @@ __device__ __forceinline__ float load_dev(const float* p) {
     return v;
 }
 
-template <int M, int GPW, int RB, bool GSUM, bool QIN>
+// LDS bytes of one wave's activation slice (AL).
+template <int M, int GPW>
+constexpr int gemv_al_bytes() { return M * GPW * 8 * 16; }
+
+template <int M, int GPW, int RB, bool AL, bool GSUM, bool QIN>
 __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
                                                     const int8_t* __restrict__ xq,
@@ -146,6 +158,9 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     constexpr int GPS = 16 / M;                  // groups per activation register set
     constexpr int NSET = (GPW + GPS - 1) / GPS;
     constexpr int NP = GPW / 2;                  // group pairs per wave
+    constexpr int ACH = M * GPW * 8;             // AL: 16-byte chunks of a wave's activations
+    constexpr int AIN = (ACH + 63) / 64;         // AL: load instructions for them
+    static_assert(!AL || (RB == 1 && !QIN), "line-wise activation loads: one row block, int8 input");
     extern __shared__ __align__(16) unsigned char smem[];
     const int W = blockDim.x >> 6;
     const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
@@ -160,10 +175,12 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     const int tile = piece ? sp.full + rem : b - npieces;
     const int c_lo = piece ? pc * NC / sp.S : 0, c_hi = piece ? (pc + 1) * NC / sp.S : NC;
     const int n0 = tile * 16 * RB;
-    // scale slice of this wave: [RB][16 rows][GPW/2] dwords (fp16 pairs), then
-    // the reduction area [W][RB][M][16]; always accessed as dwords
+    // scale slice of this wave: [RB][16 rows][GPW/2] dwords (fp16 pairs); AL: the
+    // activation slice [ACH] x 16 B; then the reduction area [W][RB][M][16]
     uint32_t* wsl = reinterpret_cast<uint32_t*>(smem) + (size_t)w * 8 * GPW * RB;
-    float* red = reinterpret_cast<float*>(smem + (size_t)W * 16 * GPW * 2 * RB);
+    uint4* axl = reinterpret_cast<uint4*>(smem + (size_t)W * 16 * GPW * 2 * RB) + (size_t)w * ACH;
+    float* red = reinterpret_cast<float*>(smem + (size_t)W * 16 * GPW * 2 * RB +
+                                          (AL ? (size_t)W * gemv_al_bytes<M, GPW>() : 0));
 
     // Load mapping of a group pair (rows n0..n0+15, 128 B each):
     //   instruction 1 covers rows 0-7, instruction 2 rows 8-15, 8 lanes per row;
@@ -220,11 +237,30 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
         uint4 ax0[NSET], ax1[NSET];
         float asc[NSET];
         float4 xv[QIN ? NSET : 1][8];
+        uint4 araw[AL ? AIN : 1];
+        if constexpr (AL) {
+            // chunk e = 64i + lane: row e/(8 GPW), group (e/8)%GPW, 16 bytes at 16(e%8)
+#pragma unroll
+            for (int i = 0; i < AIN; i++) araw[i] = make_uint4(0, 0, 0, 0);
+            if (NG > 0) {   // always true: a block of its own keeps these loads first
+#pragma unroll
+                for (int i = 0; i < AIN; i++) {
+                    int e = i * 64 + lane;
+                    e = e < ACH ? e : ACH - 1;
+                    const int row = e / (GPW * 8), grp = (e / 8) % GPW, cc = e % 8;
+                    int g = g0 + grp;
+                    g = g < NG ? g : NG - 1;
+                    araw[i] = *reinterpret_cast<const uint4*>(xq + (size_t)row * K + (size_t)g * 128 + cc * 16);
+                }
+            }
+        }
 #pragma unroll
         for (int s = 0; s < NSET; s++) {
             int g = g0 + s * GPS + jg;
             g = g < NG ? g : NG - 1;
-            if constexpr (QIN) {
+            if constexpr (AL) {
+                (void)g;
+            } else if constexpr (QIN) {
                 const float4* xp = reinterpret_cast<const float4*>(xf + (size_t)jr * K + (size_t)g * 128 + q * 32);
 #pragma unroll
                 for (int i = 0; i < 8; i++) xv[s][i] = xp[i];
@@ -261,6 +297,37 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
         if constexpr (QIN) {
 #pragma unroll
             for (int s = 0; s < NSET; s++) quant_lane(xv[s], ax0[s], ax1[s], asc[s]);
+        }
+        if constexpr (AL) {
+            // into the wave's slice, then out in the register layout: lane (j, q) of set
+            // s takes chunks 2q, 2q+1 of (row j%M, group s*GPS + j/M).  Slot of chunk cc
+            // of (row, grp): ((row*GPW + grp)*8 + (cc ^ h)), h = (row*8/Mp + grp/2) % 8
+            // with Mp = 1, 2, 4, 4 for M = 1..4.  LDS operations of one wave complete in
+            // order, so no barrier is needed; the fences only keep the compiler's order.
+            constexpr int RSH = M == 1 ? 3 : M == 2 ? 2 : 1;    // log2(8/Mp)
+#pragma unroll
+            for (int i = 0; i < AIN; i++) {
+                const int e = i * 64 + lane;
+                if (e < ACH) {
+                    const int row = e / (GPW * 8), grp = (e / 8) % GPW, cc = e % 8;
+                    const int h = ((row << RSH) + (grp >> 1)) & 7;
+                    axl[(row * GPW + grp) * 8 + (cc ^ h)] = araw[i];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int s = 0; s < NSET; s++) {
+                int grp = s * GPS + jg;
+                grp = grp < GPW ? grp : GPW - 1;          // lanes past the chunk: unused
+                const int h = ((jr << RSH) + (grp >> 1)) & 7;
+                ax0[s] = axl[(jr * GPW + grp) * 8 + ((2 * q) ^ h)];
+                ax1[s] = axl[(jr * GPW + grp) * 8 + ((2 * q + 1) ^ h)];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
 
 #pragma unroll
@@ -400,10 +467,20 @@ template <int M, int GPW, int RB, bool GSUM, bool QIN>
 hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                       const float* sa, const float* xf, int N, int K, int waves, const GemvSplit& sp,
                       hipStream_t st) {
-    const size_t smem = (size_t)waves * 16 * GPW * 2 * RB + (size_t)waves * RB * M * 16 * sizeof(float);
+    const size_t base = (size_t)waves * 16 * GPW * 2 * RB + (size_t)waves * RB * M * 16 * sizeof(float);
+    const size_t al = (size_t)waves * gemv_al_bytes<M, GPW>();
     const int grid = sp.full + sp.nrem * sp.S;
-    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, GSUM, QIN>), dim3(grid), dim3(64 * waves), smem, st, wq, ws, xq,
-                       sa, xf, y, gsum, N, K, sp);
+    // line-wise activation loads where they apply and their LDS slices fit the
+    // default 64 KB of dynamic LDS
+    if constexpr (RB == 1 && !QIN) {
+        if (base + al <= 65536) {
+            hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, true, GSUM, QIN>), dim3(grid), dim3(64 * waves), base + al,
+                               st, wq, ws, xq, sa, xf, y, gsum, N, K, sp);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, false, GSUM, QIN>), dim3(grid), dim3(64 * waves), base, st, wq, ws,
+                       xq, sa, xf, y, gsum, N, K, sp);
     return hipGetLastError();
 }
 
