@@ -409,7 +409,10 @@ def main() -> int:
     gu_bytes = gemv_kernel_bytes(M, Ngu, Kgu)
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     plan = rt4_amd.gemv_launch_plan(M, Ngu, Kgu)
-    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{plan['groups_per_wave']},{plan['row_blocks']},false,false> "
+    g_, w_, rb_ = plan["groups_per_wave"], plan["waves"], plan["row_blocks"]
+    # line-wise activation loads: one row block and their LDS slices within 64 KB (the launcher's rule)
+    al = rb_ == 1 and w_ * 16 * g_ * 2 + w_ * M * 16 * 4 + w_ * M * g_ * 8 * 16 <= 65536
+    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false> "
                           f"(gate/up GEMV, "
                           f"M={M} K={Kgu} N={Ngu}, "
                           f"{plan['waves']} waves/tile, {plan['k_splits']} K pieces/leftover tile)",
