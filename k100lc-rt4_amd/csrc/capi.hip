@@ -175,7 +175,8 @@ int default_cfg(int rows, int N, int K, rt4::GemvCfg* out) {
 int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int waves, int k_splits,
              int row_blocks, rt4::GemvCfg* out) {
     // The overrides are checked before the device is queried (argument errors
-    // come first); only the default row-block count depends on the CU count.
+    // come first), then merged into this device's defaults (which depend on the
+    // CU count).
     rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K, 0);
     if (groups_per_wave > 0) {
         c.gpw = groups_per_wave;
@@ -188,13 +189,22 @@ int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int w
     if (groups_per_wave < 0 || waves < 0 || k_splits < 0 || row_blocks < 0 || !rt4::gemv_cfg_valid(c, K))
         return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d row_blocks=%d", who,
                     groups_per_wave, waves, k_splits, row_blocks);
-    if (row_blocks == 0) {
-        rt4::GemvCfg d;
-        int rc = default_cfg(rows, N, K, &d);
-        if (rc) return rc;
-        c.rb = d.rb;
+    // the defaults of this device for whatever was left at 0
+    rt4::GemvCfg d;
+    int rc = default_cfg(rows, N, K, &d);
+    if (rc) return rc;
+    if (row_blocks > 0) d.rb = row_blocks;
+    if (groups_per_wave > 0) {
+        d.gpw = groups_per_wave;
+        const int nc = (K / 128 + d.gpw - 1) / d.gpw;
+        d.waves = nc < rt4::kGemvMaxWaves ? nc : rt4::kGemvMaxWaves;
     }
-    *out = c;
+    if (waves > 0) d.waves = waves;
+    if (k_splits > 0) d.max_split = k_splits;
+    if (!rt4::gemv_cfg_valid(d, K))
+        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d row_blocks=%d", who,
+                    groups_per_wave, waves, k_splits, row_blocks);
+    *out = d;
     return RT4_OK;
 }
 

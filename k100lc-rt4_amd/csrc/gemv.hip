@@ -524,14 +524,44 @@ hipError_t launch_rows(float* y, int32_t* gsum, const uint32_t* wq, const uint16
 
 GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
     const int NG = K / kGroup;
+    cus = cus > 0 ? cus : 256;
     GemvCfg c;
-    // Measured on MI355X over the 27B shapes (K = 5120 and 17408, N = 5120 and
-    // 17408).  One activation row: 10 groups per wave at K = 5120 (4 waves),
-    // 6 at K = 17408; two rows: 8; three or four rows (3-4x the activation
-    // registers): 4.  Waves: every chunk of the tile at once up to 8, then about
-    // a third of the chunks (each wave loops), at most 16.
-    c.gpw = rows == 1 ? (NG <= 64 ? 10 : 6) : rows == 2 ? 8 : 4;
+    // Two 16-row blocks per tile when each CU has enough tile x group work for
+    // the last round's imbalance not to matter, and the activation operand is
+    // wide enough for its reuse to pay (3-4 rows).  Measured at 4 rows: LM head
+    // (N = 248320) 114 vs 128 us; K = 17408, N = 40960 68 vs 78 us; below about
+    // 300 (32-row tile x group) units per CU it is slower (N = 17408 at K =
+    // 5120: 13.6 vs 12.7 us).  One row: slower at every N.
+    c.rb = rows >= kGemvRb2MinRows && (long long)((N + 31) / 32) * NG >= (long long)kGemvRb2Work * cus ? 2 : 1;
     const int ng_even = (NG + 1) & ~1;
+    const int ntiles = (N + 15) / 16;
+    // One row block with line-wise activation loads: 2 groups per wave while the
+    // grid is at most ~5 tiles per CU (about one residency round), with waves per
+    // tile and the leftover-tile split chosen per band.  Measured on MI355X (us,
+    // this rule vs the general one below): M=4 K=5120: N=6144 6.3 vs 7.0, 10240
+    // 8.0 vs 8.6, 17408 11.3 vs 12.2-12.8, 20480 12.5 vs 13.0; N=24576 (6 tiles
+    // per CU) 14.3 vs 15.3 with 8 waves; K=17408: N=5120 11.1 vs 11.6, 10240 20.1
+    // vs 21.7, 17408 32.4 vs 35.5; M=1 K=5120: N=5120 5.9 vs 6.2, 10240 7.6 vs
+    // 7.8, 17408 10.8 vs 10.9.  Beyond that (the LM head at 1-2 rows: 109 vs 97
+    // us) the general rule wins.
+    const double tpc = (double)ntiles / cus;
+    if (c.rb == 1 && (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
+        c.gpw = 2 < ng_even ? 2 : ng_even;
+        const int nc = (NG + c.gpw - 1) / c.gpw;
+        int w;
+        if (tpc <= 2.0 || K >= 16384) w = 16;
+        else if (tpc <= 2.75 || tpc > 5.0) w = 8;
+        else w = 4;
+        w = w < nc ? w : nc;
+        c.waves = w < kGemvMaxWaves ? w : kGemvMaxWaves;
+        c.max_split = tpc > 2.0 && tpc <= 5.0 ? 8 : 0;   // 0: pieces keep >= 32 groups
+        return c;
+    }
+    // General rule (measured before the line-wise loads): one activation row: 10
+    // groups per wave at K <= 8192, 6 above; two rows: 8; three or four: 4.
+    // Waves: every chunk of the tile at once up to 8, then about a third of the
+    // chunks (each wave loops), at most 16.
+    c.gpw = rows == 1 ? (NG <= 64 ? 10 : 6) : rows == 2 ? 8 : 4;
     if (c.gpw > ng_even) c.gpw = ng_even;
     const int nc = (NG + c.gpw - 1) / c.gpw;
     int w = (nc + 2) / 3;
@@ -539,14 +569,6 @@ GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
     w = w < nc ? w : nc;
     c.waves = w < kGemvMaxWaves ? w : kGemvMaxWaves;
     c.max_split = 0;
-    // Two 16-row blocks per tile when each CU has enough tile x group work for
-    // the last round's imbalance not to matter, and the activation operand is
-    // wide enough for its reuse to pay (3-4 rows).  Measured at 4 rows: LM head
-    // (N = 248320) 114 vs 128 us; K = 17408, N = 40960 68 vs 78 us; below about
-    // 300 (32-row tile x group) units per CU it is slower (N = 17408 at K =
-    // 5120: 13.6 vs 12.7 us).  One row: slower at every N.
-    cus = cus > 0 ? cus : 256;
-    c.rb = rows >= kGemvRb2MinRows && (long long)((N + 31) / 32) * NG >= (long long)kGemvRb2Work * cus ? 2 : 1;
     return c;
 }
 
