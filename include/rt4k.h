@@ -67,8 +67,9 @@ int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8
  * per workgroup.  When the tile count is not a multiple of the CU count, the
  * leftover tiles can be cut along K into pieces that run on otherwise idle
  * CUs: k_splits 1 keeps every tile whole, S >= 2 allows up to S pieces per
- * leftover tile.  0 selects the default for each parameter.  Every
- * configuration gives the same y bit for bit. */
+ * leftover tile.  0 selects the default for each parameter.  Configurations
+ * differ only in the order of the fp32 sums over K groups; a configuration
+ * gives the same y bit for bit on every call. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         int k_splits, int row_blocks, void* stream);
@@ -219,6 +220,16 @@ int rt4_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, v
  * over the 32-element subgroups j.  rows in [1,4], K % 128 == 0. */
 int rt4_gemv_w4a4_q(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int rows,
                     int N, int K, void* stream);
+
+/* rt4_gemv_w4a4_q with an explicit launch configuration (no counterpart in the
+ * reference, whose launch is fixed; for tuning and tests): groups_per_wave 2 or
+ * 4 K groups per wave pass, waves 1..16 waves per 16-row tile (capped at the
+ * number of such chunks), k_splits as rt4_gemv_w4a8_q_cfg (1: every tile whole,
+ * S >= 2: leftover tiles cut along K into at most S pieces).  0 selects the
+ * default for each parameter.  Configurations differ only in the order of the
+ * fp32 sums over K groups. */
+int rt4_gemv_w4a4_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
+                        int rows, int N, int K, int groups_per_wave, int waves, int k_splits, void* stream);
 
 /* The whole W4A4 decode linear: quantize x, then the GEMV.  Replaces k_gemv_w4a4
  * (src/kernels.h:25, src/k_gemv.hip:14-42).  The quantized activations go to

@@ -134,33 +134,68 @@ int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const
 // workspace and self-resetting counters (library scratch, zeroed once).
 // xf (fp32 activations, 16-byte aligned) selects the fused form that quantizes
 // inside the GEMV; otherwise xq/sa are the pre-quantized activations.
+// Workspace of a split GEMV launch (partials and self-resetting counters),
+// shared by the W4A8 and W4A4 GEMVs.  Sized once for the largest split any shape
+// can need (at most one piece per CU, 4 rows, two row blocks), so only the first
+// split launch on a device allocates.  Under graph capture nothing may be
+// allocated: if the workspace does not exist yet, the launch runs unsplit (same
+// results up to the order of the fp32 sums, less balanced).
+int gemv_split_ws(rt4::GemvSplit* sp, int cus, hipStream_t st) {
+    if (sp->nrem == 0) return RT4_OK;
+    const size_t pb = (size_t)cus * rt4::kGemvMaxRb * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
+    if (cap != hipStreamCaptureStatusNone && !(scratch_has(kSlotGemvPart, pb) && scratch_has(kSlotGemvCnt, cb))) {
+        sp->full += sp->nrem;
+        sp->nrem = 0;
+        sp->S = 1;
+        return RT4_OK;
+    }
+    void *part = nullptr, *cnt = nullptr;
+    int rc = scratch(kSlotGemvPart, pb, &part);
+    if (rc || (rc = scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
+    sp->part = static_cast<float*>(part);
+    sp->cnt = static_cast<int*>(cnt);
+    return RT4_OK;
+}
+
 int run_gemv(const char* who, int32_t* gsum, float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
              const float* sa, const float* xf, int rows, int N, int K, const rt4::GemvCfg& c, hipStream_t st) {
     int cus = 0, rc = device_cus(&cus);
     if (rc) return rc;
     rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
-    if (sp.nrem > 0) {
-        // Sized once for the largest split any shape can need (at most one piece
-        // per CU, 4 rows, two row blocks), so only the first split launch on a
-        // device allocates.
-        // Under graph capture nothing may be allocated: if the workspace does not
-        // exist yet, the launch runs unsplit (same results, less balanced).
-        const size_t pb = (size_t)cus * rt4::kGemvMaxRb * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
-        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
-        void *part = nullptr, *cnt = nullptr;
-        if (cap != hipStreamCaptureStatusNone && !(scratch_has(kSlotGemvPart, pb) && scratch_has(kSlotGemvCnt, cb))) {
-            sp.full += sp.nrem;
-            sp.nrem = 0;
-            sp.S = 1;
-        } else {
-            if ((rc = scratch(kSlotGemvPart, pb, &part))) return rc;
-            if ((rc = scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
-            sp.part = static_cast<float*>(part);
-            sp.cnt = static_cast<int*>(cnt);
-        }
-    }
+    if ((rc = gemv_split_ws(&sp, cus, st))) return rc;
     return hip_status(rt4::launch_gemv_w4a8(y, gsum, wq, ws, xq, sa, xf, rows, N, K, c, sp, st), who);
+}
+
+int run_gemv4(const char* who, float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
+              int rows, int N, int K, const rt4::GemvCfg& c, hipStream_t st) {
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
+    if ((rc = gemv_split_ws(&sp, cus, st))) return rc;
+    return hip_status(rt4::launch_gemv_w4a4(y, wq, ws, aq, sa, rows, N, K, c, sp, st), who);
+}
+
+// W4A4 GEMV configuration: this device's default with the caller's overrides
+// (0 keeps a default), the overrides checked before the device is queried.
+int gemv4_cfg(const char* who, int rows, int N, int K, int groups_per_wave, int waves, int k_splits,
+              rt4::GemvCfg* out) {
+    if ((groups_per_wave != 0 && groups_per_wave != 2 && groups_per_wave != 4) || waves < 0 ||
+        waves > rt4::kGemvMaxWaves || k_splits < 0 || k_splits > rt4::kGemvMaxSplit)
+        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d", who, groups_per_wave,
+                    waves, k_splits);
+    int cus = 0, rc = device_cus(&cus);
+    if (rc) return rc;
+    rt4::GemvCfg c = rt4::gemv4_default_cfg(rows, N, K, cus);
+    if (groups_per_wave > 0) c.gpw = groups_per_wave;
+    if (waves > 0) c.waves = waves;
+    if (k_splits > 0) c.max_split = k_splits;
+    if (!rt4::gemv4_cfg_valid(c))
+        return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d", who, groups_per_wave,
+                    waves, k_splits);
+    *out = c;
+    return RT4_OK;
 }
 
 // The default launch configuration of a shape on the current device.
@@ -374,14 +409,21 @@ int rt4_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, v
     return hip_status(rt4::launch_quant_act_a4(aq, sa, x, rows, K, as_stream(stream)), "rt4_quant_act_a4 launch");
 }
 
-int rt4_gemv_w4a4_q(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int rows,
-                    int N, int K, void* stream) {
+int rt4_gemv_w4a4_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
+                        int rows, int N, int K, int groups_per_wave, int waves, int k_splits, void* stream) {
     if (!y || !wq || !ws || !aq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a4: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a4", rows, N, K);
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(aq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
         return fail(RT4_E_ARG, "rt4_gemv_w4a4: misaligned pointer (wq and aq need 16 bytes)");
-    return hip_status(rt4::launch_gemv_w4a4(y, wq, ws, aq, sa, rows, N, K, as_stream(stream)), "rt4_gemv_w4a4 launch");
+    rt4::GemvCfg c;
+    if ((rc = gemv4_cfg("rt4_gemv_w4a4", rows, N, K, groups_per_wave, waves, k_splits, &c))) return rc;
+    return run_gemv4("rt4_gemv_w4a4 launch", y, wq, ws, aq, sa, rows, N, K, c, as_stream(stream));
+}
+
+int rt4_gemv_w4a4_q(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int rows,
+                    int N, int K, void* stream) {
+    return rt4_gemv_w4a4_q_cfg(y, wq, ws, aq, sa, rows, N, K, 0, 0, 0, stream);
 }
 
 int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N, int K,
@@ -397,9 +439,10 @@ int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     hipStream_t st = as_stream(stream);
     hipError_t e = rt4::launch_quant_act_a4(static_cast<uint32_t*>(q), static_cast<float*>(s), x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a4 quant launch");
-    return hip_status(rt4::launch_gemv_w4a4(y, wq, ws, static_cast<const uint32_t*>(q), static_cast<const float*>(s),
-                                            rows, N, K, st),
-                      "k_gemv_w4a4 launch");
+    rt4::GemvCfg c;
+    if ((rc = gemv4_cfg("k_gemv_w4a4", rows, N, K, 0, 0, 0, &c))) return rc;
+    return run_gemv4("k_gemv_w4a4 launch", y, wq, ws, static_cast<const uint32_t*>(q), static_cast<const float*>(s),
+                     rows, N, K, c, st);
 }
 
 int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint32_t* aq, const float* asc_gm, int M,

@@ -45,8 +45,8 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
                                                     const uint16_t* __restrict__ ws,
                                                     const uint32_t* __restrict__ aq,
                                                     const float* __restrict__ sa,
-                                                    float* __restrict__ y, int N, int K) {
-    static_assert(GPW == 4, "the chunk's activations are one 16-byte slot per lane");
+                                                    float* __restrict__ y, int N, int K, GemvSplit sp) {
+    static_assert(GPW == 2 || GPW == 4, "a chunk's activations: at most one 16-byte slot per lane");
     constexpr int NP = GPW / 2;                  // group pairs per wave
     extern __shared__ __align__(16) unsigned char smem[];
     const int W = blockDim.x >> 6;
@@ -54,7 +54,14 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
     const int j = lane & 15, q = lane >> 4;
     const int NG = K >> 7, RS = K >> 1, KD = K >> 3, NS = K >> 5;
     const int NC = (NG + GPW - 1) / GPW;
-    const int n0 = blockIdx.x * 16;
+    // Workgroups [0, npieces) each take one K range of a remainder tile; the rest
+    // take whole tiles (the W4A8 GEMV's split, gemv_split).
+    const int b = blockIdx.x, npieces = sp.nrem * sp.S;
+    const bool piece = b < npieces;
+    const int rem = piece ? b / sp.S : 0, pc = piece ? b % sp.S : 0;
+    const int tile = piece ? sp.full + rem : b - npieces;
+    const int c_lo = piece ? pc * NC / sp.S : 0, c_hi = piece ? (pc + 1) * NC / sp.S : NC;
+    const int n0 = tile * 16;
     // LDS: [W] weight-scale slices ([16 rows][GPW/2] dwords), [W] code slices
     // (kA4Slots + 1 zero slot, 16 B each), [W] scale slices (kA4Slots floats), then
     // the reduction area [W][M][16]
@@ -79,23 +86,23 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
     const unsigned char* p2 = reinterpret_cast<const unsigned char*>(wq) + (size_t)r2 * RS + (lo ? 4 + q : q) * 16;
     const int rj = n0 + j < N ? n0 + j : N - 1;
     // activation operand of this lane: row am of subgroup q, used iff j/4 == q;
-    // for group u it is slot (am*4 + u)*4 + q, the zero slot off the diagonal
+    // for group u it is slot (am*GPW + u)*4 + q, the zero slot off the diagonal
     const int am = j & 3;
     const bool aon = (j >> 2) == q && am < M;
-    // the chunk's load: lane l < 16M takes row l/16, group (l/4)%4, subgroup l%4
-    const int lr = lane >> 4, lu = (lane >> 2) & 3, ls = lane & 3;
-    const bool lon = lane < 16 * M;
+    // the chunk's load: lane l < 4*GPW*M takes row l/(4 GPW), group (l/4)%GPW, subgroup l%4
+    const int lr = lane / (4 * GPW), lu = (lane >> 2) % GPW, ls = lane & 3;
+    const bool lon = lane < 4 * GPW * M;
     const uint32_t* lrow = aq + (size_t)(lon ? lr : 0) * KD + 4 * ls;   // + 16 g
     const float* lsrow = sa + (size_t)(lon ? lr : 0) * NS + ls;         // + 4 g
     // this lane's scale in the fold layout (lane 16G + r: row r, subgroup G)
-    const int sslot = j < M ? (j * 4) * 4 + q : -1;                      // + 4 u
+    const int sslot = j < M ? (j * GPW) * 4 + q : -1;                    // + 4 u
     const v4i zero = {0, 0, 0, 0};
 
     float yacc[M];
 #pragma unroll
     for (int r = 0; r < M; r++) yacc[r] = 0.f;
 
-    for (int c = w; c < NC; c += W) {
+    for (int c = c_lo + w; c < c_hi; c += W) {
         const int g0 = uniform(c * GPW);
         // (1) weight scales of this wave: 16 rows x GPW fp16, as dwords (even NG)
         //     or as halves (odd NG)
@@ -150,7 +157,7 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
         float as[GPW];
 #pragma unroll
         for (int u = 0; u < GPW; u++) {
-            av[u] = acl[aon ? (am * 4 + u) * 4 + q : kA4Slots];
+            av[u] = acl[aon ? (am * GPW + u) * 4 + q : kA4Slots];
             const float sv = asl[(sslot >= 0 ? sslot : 0) + 4 * u];
             as[u] = sslot >= 0 ? sv : 0.f;
         }
@@ -210,36 +217,84 @@ __global__ __launch_bounds__(1024) void gemv_w4a4_k(const uint32_t* __restrict__
 #pragma unroll
         for (int r = 0; r < M; r++) red[(w * M + r) * 16 + lane] = yacc[r];
     __syncthreads();
-    if (threadIdx.x < M * 16) {
-        const int cl = threadIdx.x & 15, rr = threadIdx.x >> 4;
-        float tot = 0.f;
+    const int cl = threadIdx.x & 15, rr = threadIdx.x >> 4;
+    const bool out = threadIdx.x < M * 16;
+    float tot = 0.f;
+    if (out)
         for (int v = 0; v < W; v++) tot += red[(v * M + rr) * 16 + cl];
-        if (n0 + cl < N) y[(size_t)rr * N + n0 + cl] = tot;
+    if (!piece) {
+        if (out && n0 + cl < N) y[(size_t)rr * N + n0 + cl] = tot;
+        return;
     }
+    // A K range of a split tile: publish the partial, count the pieces in; the
+    // last one sums all pieces in order and resets the counter for the next call.
+    __shared__ int s_last;
+    if (out) store_dev(sp.part + (size_t)b * M * 16 + threadIdx.x, tot);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(sp.cnt + rem, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sp.S - 1;
+    __syncthreads();
+    if (!s_last) return;
+    if (out) {
+        float sum = 0.f;
+        for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + (size_t)(rem * sp.S + v) * M * 16 + threadIdx.x);
+        if (n0 + cl < N) y[(size_t)rr * N + n0 + cl] = sum;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + rem, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int M, int GPW>
+hipError_t launch_g4(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int N,
+                     int K, int waves, const GemvSplit& sp, hipStream_t st) {
+    const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * (kA4Slots + 1) * 16 +
+                        (size_t)waves * kA4Slots * sizeof(float) + (size_t)waves * M * 16 * sizeof(float);
+    const int grid = sp.full + sp.nrem * sp.S;
+    hipLaunchKernelGGL((gemv_w4a4_k<M, GPW>), dim3(grid), dim3(64 * waves), smem, st, wq, ws, aq, sa, y, N, K, sp);
+    return hipGetLastError();
 }
 
 template <int M>
 hipError_t launch_m4(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa, int N,
-                     int K, hipStream_t st) {
-    constexpr int GPW = 4;
-    const int NG = K / 128, NC = (NG + GPW - 1) / GPW;
-    const int waves = NC < 8 ? NC : 8;
-    const size_t smem = (size_t)waves * 16 * GPW * 2 + (size_t)waves * (kA4Slots + 1) * 16 +
-                        (size_t)waves * kA4Slots * sizeof(float) + (size_t)waves * M * 16 * sizeof(float);
-    hipLaunchKernelGGL((gemv_w4a4_k<M, GPW>), dim3((N + 15) / 16), dim3(64 * waves), smem, st, wq, ws, aq, sa, y, N,
-                       K);
-    return hipGetLastError();
+                     int K, const GemvCfg& c, const GemvSplit& sp, hipStream_t st) {
+    const int NC = (K / 128 + c.gpw - 1) / c.gpw;
+    const int waves = c.waves < NC ? c.waves : NC;
+    return c.gpw == 2 ? launch_g4<M, 2>(y, wq, ws, aq, sa, N, K, waves, sp, st)
+                      : launch_g4<M, 4>(y, wq, ws, aq, sa, N, K, waves, sp, st);
 }
 
 }  // namespace
 
+GemvCfg gemv4_default_cfg(int rows, int N, int K, int cus) {
+    (void)rows;
+    (void)K;
+    cus = cus > 0 ? cus : 256;
+    const double tpc = (double)((N + 15) / 16) / cus;   // 16-row tiles per CU
+    // Measured bands of tiles per CU (MI355X, K = 5120 unless noted, us, this
+    // choice vs the next best): up to 2, 16 waves and deep-K pieces (N = 5120 at
+    // K = 17408: 11.0 vs 12.0); up to 3.5, 8 waves and at most 4 pieces per
+    // leftover tile (N = 8704: 7.6 vs 8.3 whole, 9.4 with 8 pieces); up to 5,
+    // 4 waves and 4 pieces (N = 17408: 11.4 vs 12.2); up to 40, 8 waves, tiles
+    // whole (N = 34816: 19.5 vs 19.8); beyond, four groups per wave and 4 waves
+    // (N = 248320: 116 vs 117-119).
+    if (tpc <= 2.0) return GemvCfg{2, 16, 0, 1};
+    if (tpc <= 3.5) return GemvCfg{2, 8, 4, 1};
+    if (tpc <= 5.0) return GemvCfg{2, 4, 4, 1};
+    if (tpc <= 40.0) return GemvCfg{2, 8, 1, 1};
+    return GemvCfg{4, 4, 0, 1};
+}
+
+bool gemv4_cfg_valid(const GemvCfg& c) {
+    return (c.gpw == 2 || c.gpw == 4) && c.waves >= 1 && c.waves <= kGemvMaxWaves && c.max_split >= 0 &&
+           c.max_split <= kGemvMaxSplit && c.rb == 1;
+}
+
 hipError_t launch_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
-                            int rows, int N, int K, hipStream_t st) {
+                            int rows, int N, int K, const GemvCfg& c, const GemvSplit& sp, hipStream_t st) {
     switch (rows) {
-        case 1: return launch_m4<1>(y, wq, ws, aq, sa, N, K, st);
-        case 2: return launch_m4<2>(y, wq, ws, aq, sa, N, K, st);
-        case 3: return launch_m4<3>(y, wq, ws, aq, sa, N, K, st);
-        case 4: return launch_m4<4>(y, wq, ws, aq, sa, N, K, st);
+        case 1: return launch_m4<1>(y, wq, ws, aq, sa, N, K, c, sp, st);
+        case 2: return launch_m4<2>(y, wq, ws, aq, sa, N, K, c, sp, st);
+        case 3: return launch_m4<3>(y, wq, ws, aq, sa, N, K, c, sp, st);
+        case 4: return launch_m4<4>(y, wq, ws, aq, sa, N, K, c, sp, st);
     }
     return hipErrorInvalidValue;
 }

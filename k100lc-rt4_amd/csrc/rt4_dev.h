@@ -49,4 +49,17 @@ __device__ __forceinline__ uint32_t odd_x16(uint32_t w) { return w & 0xF0F0F0F0u
 // Saturating helpers for the quantizers (same clamp order as the reference).
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v > hi ? hi : (v < lo ? lo : v); }
 
+// Agent-coherent (sc1) 4-byte vector store / load of split-tile partials, each
+// with its wait in the same asm statement: the store has reached the coherent
+// level before the counter increment that publishes it, and the load's value is
+// valid before use.  (A release fence would write back the whole L2 instead.)
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0) expcnt(0)" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    float v;
+    asm volatile("global_load_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(v) : "v"(p) : "memory");
+    return v;
+}
+
 }  // namespace rt4

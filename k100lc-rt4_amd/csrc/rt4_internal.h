@@ -34,6 +34,7 @@ struct GemvCfg {
     int rb;     // 16-row blocks per tile (1 or 2): a wave applies its activations to rb blocks
 };
 constexpr int kGemvMaxWaves = 16;
+constexpr int kGemvMaxSplit = 64;      // largest k_splits override
 constexpr int kGemvMaxRb = 2;
 constexpr int kGemvRb2MinRows = 3;     // default rb = 2 needs this many activation rows
 constexpr int kGemvRb2Work = 320;      // and this many (32-row tile x K group) units per CU
@@ -56,9 +57,13 @@ hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const u
                             const GemvCfg& cfg, const GemvSplit& sp, hipStream_t st);
 
 // ---- W4A4 decode GEMV (gemv4.hip): y f32 [rows][N] from RT4 weights and int4
-// activation codes aq u32 [rows][K/8] with scales sa f32 [rows][K/32]
+// activation codes aq u32 [rows][K/8] with scales sa f32 [rows][K/32].  Tiles of
+// 16 rows (rb 1), gpw 2 or 4, waves capped at the chunk count; leftover tiles cut
+// along K as gemv_split plans (partials nrem*S*rows*16 floats).
+GemvCfg gemv4_default_cfg(int rows, int N, int K, int cus);
+bool gemv4_cfg_valid(const GemvCfg& c);
 hipError_t launch_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const uint32_t* aq, const float* sa,
-                            int rows, int N, int K, hipStream_t st);
+                            int rows, int N, int K, const GemvCfg& c, const GemvSplit& sp, hipStream_t st);
 
 // ---- prefill GEMM (gemm.hip)
 // C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],

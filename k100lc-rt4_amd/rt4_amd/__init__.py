@@ -31,7 +31,7 @@ C_EXPORTS = (
     "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
     "rt4_gemv_w4a8_groupsums",
     "rt4_gemv_w4a8", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
-    "rt4_make_group_major", "rt4_quant_rows_a4", "rt4_quant_act_a4", "rt4_gemv_w4a4_q", "rt4_gemv_w4a4",
+    "rt4_make_group_major", "rt4_quant_rows_a4", "rt4_quant_act_a4", "rt4_gemv_w4a4_q", "rt4_gemv_w4a4_q_cfg", "rt4_gemv_w4a4",
     "rt4_gemm_w4a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
     "rt4_attn_q_quant", "rt4_kv_append_k", "rt4_kv_append_v", "rt4_attention_prefill",
@@ -65,6 +65,7 @@ _SIGS = {
     "rt4_quant_act_a8": [_P, _P, _P, _P, _I, _I, _P],
     "rt4_quant_act_a4": [_P, _P, _P, _I, _I, _P],
     "rt4_gemv_w4a4_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a4_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "rt4_gemv_w4a4": [_P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemm_w4a4": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
@@ -284,13 +285,17 @@ def quant_act_a4(x):
     return aq, sa
 
 
-def gemv_w4a4_q(wq, ws, aq, sa, out=None):
-    """W4A4 GEMV on int4 activation codes aq int32 [rows, K/8], sa f32 [rows, K/32]."""
+def gemv_w4a4_q(wq, ws, aq, sa, out=None, groups_per_wave: int = 0, waves: int = 0, k_splits: int = 0):
+    """W4A4 GEMV on int4 activation codes aq int32 [rows, K/8], sa f32 [rows, K/32].
+
+    groups_per_wave (2 or 4) / waves (1..16) / k_splits (1: tiles whole) override
+    the launch configuration (0 keeps the default)."""
     torch = _torch()
     rows, KD = aq.shape
     N = wq.shape[0]
     y = out if out is not None else _empty((rows, N), torch.float32, aq.device)
-    _check(lib().rt4_gemv_w4a4_q(_ptr(y), _ptr(wq), _ptr(ws), _ptr(aq), _ptr(sa), rows, N, KD * 8, _stream()))
+    _check(lib().rt4_gemv_w4a4_q_cfg(_ptr(y), _ptr(wq), _ptr(ws), _ptr(aq), _ptr(sa), rows, N, KD * 8,
+                                     groups_per_wave, waves, k_splits, _stream()))
     return y
 
 

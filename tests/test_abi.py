@@ -65,6 +65,10 @@ def test_gemv_null_and_config_errors(rt4):
     assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 65, 0, None) == 2
     assert L.rt4_gemv_w4a8_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 0, 3, None) == 2
     assert "config" in L.rt4_last_error().decode()
+    assert L.rt4_gemv_w4a4_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 3, 0, 0, None) == 2
+    assert L.rt4_gemv_w4a4_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 17, 0, None) == 2
+    assert L.rt4_gemv_w4a4_q_cfg(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 1, 64, 256, 2, 1, 65, None) == 2
+    assert "k_splits=65" in L.rt4_last_error().decode()
 
 
 def test_quant_errors(rt4):

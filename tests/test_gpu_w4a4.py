@@ -85,6 +85,29 @@ def test_gemv_w4a4_against_oracle(rt4, orc, torch_gpu, M, N, K):
     assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K", [(4, 200, 2048), (3, 33, 384), (1, 48, 1920), (2, 40, 128), (4, 64, 17408),
+                                   (4, 4176, 8192), (1, 4100, 17408)])
+def test_gemv_w4a4_configs_agree(rt4, orc, torch_gpu, M, N, K):
+    """Every launch configuration (groups per wave 2 or 4, 1..16 waves, leftover
+    tiles whole or cut along K) meets the oracle; odd group counts and chunks cut
+    by the end of K included.  The configurations differ only in the order of the
+    fp32 sums over groups; one configuration repeats bit for bit (a split launch
+    leaves its counters at zero for the next)."""
+    print(f"case gemv_w4a4 configs M={M} N={N} K={K}", flush=True)
+    c = workload.gemv_case(seed=45, M=M, N=N, K=K)
+    x = _acts4(np.random.default_rng(45), M, K)
+    wq, ws = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["ws"])
+    aq, sa = rt4.quant_act_a4(dev(torch_gpu, x))
+    ref = orc.gemv_w4a4(c["wq"], c["ws"], x)
+    for g, w, s in [(2, 1, 1), (2, 2, 0), (2, 3, 5), (2, 8, 64), (2, 16, 2), (4, 1, 0), (4, 2, 64), (4, 3, 1),
+                    (4, 8, 3), (4, 16, 0)]:
+        y = rt4.gemv_w4a4_q(wq, ws, aq, sa, groups_per_wave=g, waves=w, k_splits=s)
+        y2 = rt4.gemv_w4a4_q(wq, ws, aq, sa, groups_per_wave=g, waves=w, k_splits=s)
+        torch_gpu.cuda.synchronize()
+        assert rel_l2(host(y), ref) < TIGHT, (g, w, s)
+        assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32)), (g, w, s)
+
+
 @pytest.mark.parametrize("name", ["c0", "c1_gate_up", "c1_down"])
 def test_gemv_w4a4_benchmark_shapes(rt4, orc, torch_gpu, name):
     M, N, K = workload.GEMV_SHAPES[name]
