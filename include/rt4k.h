@@ -7,6 +7,14 @@
  * Every entry point is asynchronous on `stream` and returns RT4_OK or an error
  * code; rt4_last_error() then describes the failure (thread-local).
  *
+ * Library scratch: the drop-in linears' quantized activations, the split
+ * workspaces of the GEMVs (W4A8 and W4A4 share one, partials plus counters that
+ * every launch leaves at zero), of the GEMM and of the attention prefill are one
+ * buffer per device and kind, grown on demand like the reference's static
+ * scratch (src/k_gemv.hip:16-23).  Calls that may run at the same time on one
+ * device (different streams) therefore race on it; the caller orders them, as
+ * it must for the reference.
+ *
  * Formats (docs/FORMAT.md:61-73 of the reference, unchanged here):
  *   wq   uint32 [N][K/8]   RT4 int4 weights: dword d holds k = 8d..8d+7, nibble e
  *                          = bits 4e..4e+3, two's complement, low nibble first.
