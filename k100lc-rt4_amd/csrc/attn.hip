@@ -192,6 +192,76 @@ __global__ __launch_bounds__(64) void kv_stage_v_k(float* __restrict__ stage, co
     }
 }
 
+// The same two phases for the attention kernels' V tile of BG = 64 keys, with
+// 256 threads per (head, 64 dims, tile): wave p owns keys 16p..16p+15, so each
+// lane loads its 16 values once (coalesced across dims), the four waves combine
+// their maxima through LDS and each lane packs its two code dwords from
+// registers.  Values, scale and codes are those of kv_append_v_k: the maximum
+// of a set does not depend on the order it is taken in, and keys past the valid
+// ones are 0 in both.
+__global__ __launch_bounds__(256) void kv_append_v64_k(uint32_t* __restrict__ vc, float* __restrict__ vsc,
+                                                       const float* __restrict__ stage,
+                                                       const float* __restrict__ vf, int t0, int T, int H, int D,
+                                                       int kv_total) {
+    constexpr int BG = 64;
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    const int h = blockIdx.x, d = blockIdx.y * 64 + lane, ti = blockIdx.z;
+    const bool dv = d < D;
+    const int first = t0 / BG, tile = first + ti, slot0 = ti == 0 ? t0 % BG : 0;
+    const int done = ti == 0 ? 0 : (BG - t0 % BG) + (ti - 1) * BG;  // new values before this tile
+    const int n = (T - done < BG - slot0) ? (T - done) : (BG - slot0);
+    const int nval = slot0 + n;
+    const float* st = stage + (size_t)h * BG * D + d;
+    const float* src = vf + ((size_t)(done - slot0) * H + h) * D + d;  // slot i >= slot0 -> src[i*H*D]
+    float v[16];
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int k = 16 * p + e;
+        float x = 0.f;
+        if (dv && k < nval) x = k < slot0 ? st[(size_t)k * D] : src[(size_t)k * H * D];
+        v[e] = x;
+        amax = fmaxf(amax, fabsf(x));
+    }
+    red[p][lane] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0][lane], red[1][lane]), fmaxf(red[2][lane], red[3][lane]));
+    if (!dv) return;
+    const float s = amax > 0.f ? amax / 7.f : 1.f;
+    if (p == 0) vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
+    uint32_t* out = vc + ((size_t)h * (kv_total / 8) + (size_t)tile * (BG / 8)) * D + d;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) w |= code4(v[8 * j + e], s) << (4 * e);
+        out[(size_t)(2 * p + j) * D] = w;
+    }
+}
+
+// Phase 2 for BG = 64: wave p restores slots 16p..16p+15 (see kv_stage_v_k).
+__global__ __launch_bounds__(256) void kv_stage_v64_k(float* __restrict__ stage, const float* __restrict__ vf,
+                                                      int t0, int T, int H, int D) {
+    constexpr int BG = 64;
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    const int h = blockIdx.x, d = blockIdx.y * 64 + lane;
+    if (d >= D) return;
+    const int first = t0 / BG, last = (t0 + T - 1) / BG;
+    const int nval = (t0 + T - 1) % BG + 1;
+    const int lo_last = last == first ? t0 % BG : 0;
+    const int lo_prev = last - 1 == first ? t0 % BG : 0;
+    float* st = stage + (size_t)h * BG * D + d;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int k = 16 * p + e;
+        int tok = -1;  // index of the new value that ends up in slot k
+        if (k >= lo_last && k < nval) tok = last * BG + k - t0;
+        else if (k >= nval && last > first && k >= lo_prev) tok = (last - 1) * BG + k - t0;
+        if (tok >= 0) st[(size_t)k * D] = vf[((size_t)tok * H + h) * D + d];
+    }
+}
+
 // ---------------------------------------------------------------- prefill --
 
 __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__ qq,
@@ -517,6 +587,14 @@ hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const floa
                               int D, int BG, int kv_total, hipStream_t st) {
     if (T <= 0) return hipSuccess;
     const int ntile = (t0 + T - 1) / BG - t0 / BG + 1;
+    if (BG == 64) {   // the attention kernels' V tile
+        hipLaunchKernelGGL(kv_append_v64_k, dim3(H, (D + 63) / 64, ntile), dim3(256), 0, st, vc, vsc, stage, vf, t0,
+                           T, H, D, kv_total);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kv_stage_v64_k, dim3(H, (D + 63) / 64), dim3(256), 0, st, stage, vf, t0, T, H, D);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(kv_append_v_k, dim3(H, (D + 63) / 64, ntile), dim3(64), 0, st, vc, vsc, stage, vf, t0, T, H,
                        D, BG, kv_total);
     const hipError_t e = hipGetLastError();

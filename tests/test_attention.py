@@ -293,6 +293,33 @@ def test_feeders_bit_exact(rt4, orc, torch_gpu, T, n_kv, H, KVH, steps):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("BG,D", [(32, 256), (64, 200), (128, 256)])
+def test_kv_append_v_other_tiles(rt4, orc, torch_gpu, BG, D):
+    """V tiles other than 64 keys (the generic kernels) and a dim count that is not
+    a multiple of 64 (the 64-key kernels' tail lanes), in several appends."""
+    print(f"case kv_append_v BG={BG} D={D}", flush=True)
+    rng = np.random.default_rng(17 + BG)
+    KVH, n_kv = 2, 300
+    cap = (n_kv + BG - 1) // BG * BG
+    v = rng.standard_normal((n_kv, KVH, D)).astype(np.float32)
+    v[5:9, 0, :] = 0.0
+    vc = torch_gpu.zeros((KVH, cap // 8, D), dtype=torch_gpu.int32, device="cuda")
+    vsc = torch_gpu.ones((KVH, cap // BG, D), dtype=torch_gpu.float32, device="cuda")
+    stage = torch_gpu.zeros((KVH, BG, D), dtype=torch_gpu.float32, device="cuda")
+    vc_o = np.zeros((KVH, cap // 8, D), np.uint32)
+    vsc_o = np.ones((KVH, cap // BG, D), np.float32)
+    st_o = np.zeros((KVH, BG, D), np.float32)
+    vd = dev(torch_gpu, v)
+    for a, b in [(0, 7), (7, 70), (70, 71), (71, 300)]:
+        rt4.kv_append_v(vc, vsc, stage, vd[a:b].contiguous(), a)
+        orc.kv_append_v(vc_o, vsc_o, st_o, v[a:b], a, cap)
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(host(vc).view(np.uint32), vc_o)
+    assert np.array_equal(host(vsc).view(np.uint32), vsc_o.view(np.uint32))
+    assert np.array_equal(host(stage).view(np.uint32), st_o.view(np.uint32))
+
+
+@pytest.mark.gpu
 def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
     """The reference's own k_attn_q_quant / k_kv_append_k / k_kv_append_v built for gfx950."""
     print("case feeders vs reference kernels", flush=True)
