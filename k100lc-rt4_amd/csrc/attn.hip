@@ -535,22 +535,36 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 
 // Combine of the KV splits of one (head, query row): with M the largest running
 // max, out = Σ_s O_s 2^(m_s - M) / Σ_s L_s 2^(m_s - M), splits in order.
-// grid (n_q, H), block 256 (one thread per dim).
+// grid (n_q / 4, H), block 256 (one thread per dim); each thread combines 4
+// query rows side by side, so its loads of a split are independent.
+constexpr int kCombRows = 4;
 __global__ __launch_bounds__(256) void fa_combine_k(float* __restrict__ out, const float* __restrict__ opart,
                                                    const float2* __restrict__ mlpart, int n_q, int nsplit) {
-    const int row = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+    const int row0 = blockIdx.x * kCombRows, head = blockIdx.y, d = threadIdx.x;
     const int H = gridDim.y;
-    float M = -__builtin_inff();
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, mlpart[((size_t)s * H + head) * n_q + row].x);
-    float o = 0.f, l = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const size_t prow = ((size_t)s * H + head) * n_q + row;
-        const float2 ml = mlpart[prow];
-        const float a = exp2f(ml.x - M);
-        o = fmaf(a, opart[prow * HD + d], o);
-        l = fmaf(a, ml.y, l);
+    float M[kCombRows], o[kCombRows], l[kCombRows];
+#pragma unroll
+    for (int r = 0; r < kCombRows; r++) {
+        M[r] = -__builtin_inff();
+        o[r] = 0.f;
+        l[r] = 0.f;
     }
-    out[((size_t)head * n_q + row) * HD + d] = l > 0.f ? o / l : 0.f;
+    for (int s = 0; s < nsplit; s++)
+#pragma unroll
+        for (int r = 0; r < kCombRows; r++) M[r] = fmaxf(M[r], mlpart[((size_t)s * H + head) * n_q + row0 + r].x);
+    for (int s = 0; s < nsplit; s++) {
+#pragma unroll
+        for (int r = 0; r < kCombRows; r++) {
+            const size_t prow = ((size_t)s * H + head) * n_q + row0 + r;
+            const float2 ml = mlpart[prow];
+            const float a = exp2f(ml.x - M[r]);
+            o[r] = fmaf(a, opart[prow * HD + d], o[r]);
+            l[r] = fmaf(a, ml.y, l[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kCombRows; r++)
+        out[((size_t)head * n_q + row0 + r) * HD + d] = l[r] > 0.f ? o[r] / l[r] : 0.f;
 }
 
 // -------------------------------------------------------------- launchers --
@@ -633,7 +647,8 @@ hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, cons
     hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads, nsplit), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc,
                        out, n_q, n_kv, off, n_tile, ratio, kv_cap, nsplit, opart, mlpart);
     if (nsplit > 1)
-        hipLaunchKernelGGL(fa_combine_k, dim3(n_q, n_heads), dim3(256), 0, st, out, opart, mlpart, n_q, nsplit);
+        hipLaunchKernelGGL(fa_combine_k, dim3(n_q / kCombRows, n_heads), dim3(256), 0, st, out, opart, mlpart, n_q,
+                           nsplit);   // n_q is a multiple of 64
     return hipGetLastError();
 }
 
