@@ -535,9 +535,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 
 // Combine of the KV splits of one (head, query row): with M the largest running
 // max, out = Σ_s O_s 2^(m_s - M) / Σ_s L_s 2^(m_s - M), splits in order.
-// grid (n_q / 4, H), block 256 (one thread per dim); each thread combines 4
+// grid (n_q / 8, H), block 256 (one thread per dim); each thread combines 8
 // query rows side by side, so its loads of a split are independent.
-constexpr int kCombRows = 4;
+constexpr int kCombRows = 8;
 __global__ __launch_bounds__(256) void fa_combine_k(float* __restrict__ out, const float* __restrict__ opart,
                                                    const float2* __restrict__ mlpart, int n_q, int nsplit) {
     const int row0 = blockIdx.x * kCombRows, head = blockIdx.y, d = threadIdx.x;
