@@ -13,7 +13,9 @@
  * buffer per device and kind, grown on demand like the reference's static
  * scratch (src/k_gemv.hip:16-23).  Calls that may run at the same time on one
  * device (different streams) therefore race on it; the caller orders them, as
- * it must for the reference.
+ * it must for the reference.  An outgrown buffer is kept allocated until the
+ * process ends (the reference frees it), so a HIP graph captured before a
+ * larger call still replays into valid memory; growth is by half at least.
  *
  * Formats (docs/FORMAT.md:61-73 of the reference, unchanged here):
  *   wq   uint32 [N][K/8]   RT4 int4 weights: dword d holds k = 8d..8d+7, nibble e

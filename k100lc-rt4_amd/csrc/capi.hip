@@ -28,9 +28,12 @@ int hip_status(hipError_t e, const char* what) {
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Library-owned device scratch, one buffer per (device, slot), grown on demand.
-// hipFree synchronizes the device, so a buffer still read by queued kernels is
-// never released early.  Not safe for concurrent calls from several threads
-// (the reference's scratch has the same property, src/k_gemv.hip:47-51).
+// A buffer that is outgrown is retired, not freed: a HIP graph captured earlier
+// keeps its address and may still be replayed (freeing it would leave such a
+// graph writing into released memory).  Growth is geometric (x1.5 at least), so
+// the retired buffers of a slot add up to at most twice its final size.  Not
+// safe for concurrent calls from several threads (the reference's scratch has
+// the same property, src/k_gemv.hip:47-51).
 enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlots = 8 };
 constexpr int kMaxDev = 64;
 struct Buf {
@@ -56,15 +59,12 @@ int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, 
     std::lock_guard<std::mutex> lk(g_mu);
     Buf& b = g_buf[dev][slot];
     if (b.cap < bytes) {
-        if (b.p) {
-            e = hipFree(b.p);
-            b.p = nullptr;
-            b.cap = 0;
-            if (e != hipSuccess) return hip_status(e, "hipFree(scratch)");
-        }
-        const size_t want = (bytes + 255) & ~size_t(255);
-        e = hipMalloc(&b.p, want);
+        const size_t grown = b.cap + b.cap / 2;
+        const size_t want = ((bytes > grown ? bytes : grown) + 255) & ~size_t(255);
+        void* p = nullptr;
+        e = hipMalloc(&p, want);
         if (e != hipSuccess) return hip_status(e, "hipMalloc(scratch)");
+        b.p = p;            // the outgrown buffer, if any, stays allocated (see above)
         b.cap = want;
         if (zero) {
             e = rt4::launch_zero_i32(static_cast<int*>(b.p), want / sizeof(int), zero_on);

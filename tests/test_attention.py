@@ -416,3 +416,34 @@ def test_attention_benchmark_shape_sampled(rt4, orc, torch_gpu):
     out, _ = check_attention(rt4, orc, torch_gpu, q, k, v, c4["H"] // c4["KVH"], ctx, n_kv, n_kv,
                              lambda h: rows, (0, 5, 6, 23))
     assert np.isfinite(out).all()
+
+
+@pytest.mark.gpu
+def test_graph_keeps_workspace_when_scratch_grows(rt4, torch_gpu):
+    """A HIP graph captured on the split-KV path holds the address of the library's
+    partial-sum workspace.  A later, larger call grows that workspace; the graph's
+    buffer must stay allocated, so its replays still give the eager result."""
+    torch = torch_gpu
+    print("case graph replay after scratch growth", flush=True)
+    rng = np.random.default_rng(23)
+    q, k, v = workload.attn_np(rng, 64, 640, 2, 1)
+    g = gpu_cache(rt4, torch, q, k, v, 64, 640)
+    kw = dict(n_kv=640, off=576, ratio=2, kv_splits=2)
+    ref = host(rt4.attention_prefill(*g[:6], **kw))
+    out = torch.empty((2, 64, HD), dtype=torch.float32, device="cuda")
+    rt4.attention_prefill(*g[:6], out=out, **kw)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rt4.attention_prefill(*g[:6], out=out, **kw)
+    # grow the workspace: 64 splits x 24 heads x 256 rows x 1 KB of partials
+    q2, k2, v2 = workload.attn_np(rng, 256, 640, 24, 4)
+    g2 = gpu_cache(rt4, torch, q2, k2, v2, 256, 640)
+    rt4.attention_prefill(*g2[:6], n_kv=640, off=384, ratio=6, kv_splits=64)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out).view(np.uint32), ref.view(np.uint32))
