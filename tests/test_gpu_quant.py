@@ -113,3 +113,79 @@ def test_quantizers_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
     oq4, osc4 = orc.quant_rows_a4(x, rows, K, G)
     assert np.array_equal(host(rq).view(np.uint32), oq4) and np.array_equal(host(q4).view(np.uint32), oq4)
     assert np.array_equal(host(rsc4), osc4) and np.array_equal(host(sc4), osc4)
+
+
+def _special_acts(M, K):
+    """Activations with IEEE special values in separate groups: +-Inf, NaN (alone
+    and beside Inf), subnormals, +-FLT_MAX, -0.0 and tiny normals."""
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    big = np.finfo(np.float32).max
+    x[0, 5], x[0, 200] = np.inf, -np.inf
+    x[1 % M, 130] = np.nan
+    x[1 % M, 256:384] = np.float32(1e-40) * rng.standard_normal(128).astype(np.float32)
+    x[2 % M, 384:512] = big * rng.choice(np.array([-1, 1], np.float32), 128)
+    x[2 % M, 512:640] = -0.0
+    x[3 % M, 640:768] = np.float32(1e-30) * rng.standard_normal(128).astype(np.float32)
+    x[3 % M, 768], x[3 % M, 769] = np.nan, np.inf
+    return x
+
+
+def test_special_values_match_reference_kernels(rt4, torch_gpu, ref_hip):
+    """IEEE special inputs: the float-to-int conversion of NaN and the scale of an
+    Inf or subnormal group are the GPU's own behaviour, so the check is against
+    the reference's quantizers built for gfx950 on the same card (codes, scales
+    and sums bit for bit), and the one-launch GEMV against quantizer + GEMV."""
+    M, K = 4, 1024
+    x_np = _special_acts(M, K)
+    x = dev(torch_gpu, x_np)
+    # decode int8 (quant_act, /127 per 128)
+    ae = torch_gpu.empty((M, K // 2), dtype=torch_gpu.int8, device="cuda")
+    ao = torch_gpu.empty_like(ae)
+    asc = torch_gpu.empty((M, K // 128), dtype=torch_gpu.float32, device="cuda")
+    asu = torch_gpu.empty((M, K // 128), dtype=torch_gpu.int32, device="cuda")
+    torch_gpu.cuda.synchronize()
+    ref_hip.ref_quant_act(P(x.data_ptr()), P(ae.data_ptr()), P(ao.data_ptr()), P(asc.data_ptr()),
+                          P(asu.data_ptr()), M, K)
+    ref_hip.ref_sync()
+    xq, sa, su = rt4.quant_act_a8(x, want_sums=True)
+    torch_gpu.cuda.synchronize()
+    q = layout.deinterleave(host(xq))
+    assert np.array_equal(q[:, 0::2], host(ae)) and np.array_equal(q[:, 1::2], host(ao))
+    assert np.array_equal(host(sa).view(np.uint32), host(asc).view(np.uint32))
+    assert np.array_equal(host(su), host(asu))
+    # the one-launch GEMV quantizes in registers: same y as quantizer + GEMV
+    c = workload.gemv_case(seed=72, M=M, N=64, K=K)
+    wq, ws = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["ws"])
+    y1 = rt4.gemv_w4a8(wq, ws, x, groups_per_wave=2, waves=4)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=2, waves=4)
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
+    # decode int4 (quant_act4, /7 per 32)
+    aq_r = torch_gpu.zeros((M, K // 2), dtype=torch_gpu.uint8, device="cuda")
+    sa_r = torch_gpu.zeros((M, K // 32), dtype=torch_gpu.float32, device="cuda")
+    torch_gpu.cuda.synchronize()
+    ref_hip.ref_quant_act4(P(x.data_ptr()), P(aq_r.data_ptr()), P(sa_r.data_ptr()), M, K)
+    ref_hip.ref_sync()
+    aq4, sa4 = rt4.quant_act_a4(x)
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(host(aq4).view(np.uint8), host(aq_r))
+    assert np.array_equal(host(sa4).view(np.uint32), host(sa_r).view(np.uint32))
+    # prefill (/119 digits and /7), G = 128
+    rows = 128
+    xp_np = np.tile(x_np, (rows // M, 1))
+    xp = dev(torch_gpu, xp_np)
+    f = lambda *s: torch_gpu.empty(s, dtype=torch_gpu.int32, device="cuda")  # noqa: E731
+    rh, rl, rq = f(rows, K // 8), f(rows, K // 8), f(rows, K // 8)
+    rsc = torch_gpu.empty((K // 128, rows), dtype=torch_gpu.float32, device="cuda")
+    rsc16, rsc4 = torch_gpu.empty_like(rsc), torch_gpu.empty_like(rsc)
+    torch_gpu.cuda.synchronize()
+    ref_hip.ref_quant_rows_a8(P(rh.data_ptr()), P(rl.data_ptr()), P(rsc.data_ptr()), P(rsc16.data_ptr()),
+                              P(xp.data_ptr()), rows, K, 128, 0, 0)
+    ref_hip.ref_quant_rows(P(rq.data_ptr()), P(rsc4.data_ptr()), P(xp.data_ptr()), rows, K, 128, 0, 0)
+    ref_hip.ref_sync()
+    qh, ql, sc, sc16 = rt4.quant_rows_a8(xp)
+    q4, sc4 = rt4.quant_rows_a4(xp)
+    torch_gpu.cuda.synchronize()
+    for ours, theirs in [(qh, rh), (ql, rl), (sc, rsc), (sc16, rsc16), (q4, rq), (sc4, rsc4)]:
+        assert np.array_equal(host(ours).view(np.uint32), host(theirs).view(np.uint32))
