@@ -320,9 +320,12 @@ def test_kv_append_v_other_tiles(rt4, orc, torch_gpu, BG, D):
 
 
 @pytest.mark.gpu
-def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
-    """The reference's own k_attn_q_quant / k_kv_append_k / k_kv_append_v built for gfx950."""
-    print("case feeders vs reference kernels", flush=True)
+@pytest.mark.parametrize("special", [False, True])
+def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip, special):
+    """The reference's own k_attn_q_quant / k_kv_append_k / k_kv_append_v built for gfx950;
+    `special` plants IEEE special values (+-Inf, NaN, subnormals, FLT_MAX, -0.0) in Q, K
+    and V, whose handling is the GPU's own and so is checked against these kernels."""
+    print(f"case feeders vs reference kernels special={special}", flush=True)
     import ctypes
     torch = torch_gpu
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
@@ -334,6 +337,16 @@ def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
     rng = np.random.default_rng(12)
     T, n_kv, H, KVH = 100, 700, 6, 2
     q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    if special:
+        big = np.finfo(np.float32).max
+        q[3, 1, 5], q[10, 2, 130], q[30, 4, 0] = np.inf, np.nan, -np.inf
+        q[20, 0, :128] = np.float32(1e-40)
+        k[50, 0, 7], k[60, 1, 200] = np.inf, np.nan
+        k[100:110, 0, :] = big
+        k[400, 1, :128] = -0.0
+        v[70, 0, 3], v[80, 1, 9], v[650, 1, 255] = np.inf, np.nan, -np.inf
+        v[300, 0, :] = np.float32(1e-40)
+        v[200:264, 1, 17] = -big
     TP, cap = 128, 704
     steps = [(0, 333), (333, 334), (334, 700)]
     ours = gpu_cache(rt4, torch, q, k, v, TP, cap, steps)
@@ -351,7 +364,7 @@ def test_feeders_against_reference_kernels(rt4, orc, torch_gpu, ref_hip):
         ref_hip.ref_kv_append_v(P(vc), P(vsc), P(st), P(vd[a:b].contiguous()), a, b - a, KVH, HD, BN, cap)
     ref_hip.ref_sync()
     for got, want in zip(ours, (qq, qs, kc, ksc, vc, vsc, st)):
-        assert torch.equal(got, want)
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32))     # bit patterns (NaN too)
 
 
 def check_attention(rt4, orc, torch, q, k, v, ratio, off, n_kv, kv_cap, rows_per_head, heads, splits=(0,)):
