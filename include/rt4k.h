@@ -16,6 +16,10 @@
  * it must for the reference.  An outgrown buffer is kept allocated until the
  * process ends (the reference frees it), so a HIP graph captured before a
  * larger call still replays into valid memory; growth is by half at least.
+ * Nothing is allocated while `stream` is being captured: a call that would
+ * have to grow a scratch buffer then fails with RT4_E_CAPTURE, except that the
+ * split GEMV and the attention prefill (automatic split count) fall back to
+ * their unsplit forms, which need no workspace.
  *
  * Formats (docs/FORMAT.md:61-73 of the reference, unchanged here):
  *   wq   uint32 [N][K/8]   RT4 int4 weights: dword d holds k = 8d..8d+7, nibble e
@@ -46,6 +50,9 @@ extern "C" {
 #define RT4_E_SHAPE 1    /* a shape precondition of the reference is violated */
 #define RT4_E_ARG 2      /* null pointer, unsupported group size or config */
 #define RT4_E_HIP 3      /* HIP runtime or kernel launch failure */
+#define RT4_E_CAPTURE 4  /* library scratch would have to grow while the stream is being
+                            captured into a HIP graph: make one eager call at the largest
+                            shape first (nothing is allocated under capture) */
 
 /* Description of the last failure on this thread ("" if none). */
 const char* rt4_last_error(void);

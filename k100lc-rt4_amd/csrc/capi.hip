@@ -51,7 +51,19 @@ bool scratch_has(Slot slot, size_t bytes) {
     return g_buf[dev][slot].cap >= bytes;
 }
 
-int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, bool zero = false) {
+// Whether work on `st` is being recorded into a HIP graph (nothing may be
+// allocated then: hipMalloc is not a graph operation).
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) return false;
+    return cap != hipStreamCaptureStatusNone;
+}
+
+// The slot's buffer, grown to at least `bytes` (counters zeroed on `st` when
+// `zero`).  Growth under stream capture is refused with RT4_E_CAPTURE: one
+// eager call at the largest shape first sizes the scratch, after which capture
+// allocates nothing.
+int scratch(Slot slot, size_t bytes, void** out, hipStream_t st, bool zero = false) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
@@ -59,6 +71,11 @@ int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, 
     std::lock_guard<std::mutex> lk(g_mu);
     Buf& b = g_buf[dev][slot];
     if (b.cap < bytes) {
+        if (capturing(st))
+            return fail(RT4_E_CAPTURE,
+                        "library scratch (slot %d) must grow from %zu to %zu bytes while the stream is being "
+                        "captured; make one eager call at this shape before capturing",
+                        (int)slot, b.cap, bytes);
         const size_t grown = b.cap + b.cap / 2;
         const size_t want = ((bytes > grown ? bytes : grown) + 255) & ~size_t(255);
         void* p = nullptr;
@@ -67,7 +84,7 @@ int scratch(Slot slot, size_t bytes, void** out, hipStream_t zero_on = nullptr, 
         b.p = p;            // the outgrown buffer, if any, stays allocated (see above)
         b.cap = want;
         if (zero) {
-            e = rt4::launch_zero_i32(static_cast<int*>(b.p), want / sizeof(int), zero_on);
+            e = rt4::launch_zero_i32(static_cast<int*>(b.p), want / sizeof(int), st);
             if (e != hipSuccess) return hip_status(e, "zeroing scratch");
         }
     }
@@ -88,8 +105,8 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) &
 // The GEMV reads weights and activations with 16-byte vector loads.
 int check_gemv_align(const char* who, const void* y, const uint32_t* wq, const uint16_t* ws,
                      const int8_t* xq, const float* sa) {
-    if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
-        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
+    if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes, ws 4)", who);
     return RT4_OK;
 }
 
@@ -97,6 +114,11 @@ int check_gemm_args(const char* who, int M, int N, int K) {
     if (M < 1 || N < 1) return fail(RT4_E_SHAPE, "%s: M=%d N=%d must be positive", who, M, N);
     if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "%s: K=%d is not a positive multiple of 128", who, K);
     if (M > 65535 * 128) return fail(RT4_E_SHAPE, "%s: M=%d too large", who, M);
+    // the kernels address a row block of A and of W with 32-bit byte offsets
+    if ((unsigned long long)M * (unsigned long long)K >= (1ull << 32) ||
+        (unsigned long long)N * (unsigned long long)(K / 2) >= (1ull << 32))
+        return fail(RT4_E_SHAPE, "%s: M*K=%llu or N*K/2=%llu bytes exceeds the 32-bit offset range", who,
+                    (unsigned long long)M * K, (unsigned long long)N * (K / 2));
     return RT4_OK;
 }
 
@@ -123,7 +145,7 @@ int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const
     if (rc) return rc;
     const rt4::GemmPlan plan = rt4::gemm_plan(M, N, K, cus);
     void *part = nullptr, *cnt = nullptr;
-    if ((rc = scratch(kSlotGemmPart, plan.part_bytes, &part))) return rc;
+    if ((rc = scratch(kSlotGemmPart, plan.part_bytes, &part, st))) return rc;
     if ((rc = scratch(kSlotGemmCnt, plan.cnt_bytes, &cnt, st, true))) return rc;
     return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, plan, static_cast<float*>(part),
                                             static_cast<int*>(cnt), st),
@@ -143,16 +165,14 @@ int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const
 int gemv_split_ws(rt4::GemvSplit* sp, int cus, hipStream_t st) {
     if (sp->nrem == 0) return RT4_OK;
     const size_t pb = (size_t)cus * rt4::kGemvMaxRb * 4 * 16 * sizeof(float), cb = (size_t)cus * sizeof(int);
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
-    if (cap != hipStreamCaptureStatusNone && !(scratch_has(kSlotGemvPart, pb) && scratch_has(kSlotGemvCnt, cb))) {
+    if (capturing(st) && !(scratch_has(kSlotGemvPart, pb) && scratch_has(kSlotGemvCnt, cb))) {
         sp->full += sp->nrem;
         sp->nrem = 0;
         sp->S = 1;
         return RT4_OK;
     }
     void *part = nullptr, *cnt = nullptr;
-    int rc = scratch(kSlotGemvPart, pb, &part);
+    int rc = scratch(kSlotGemvPart, pb, &part, st);
     if (rc || (rc = scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
     sp->part = static_cast<float*>(part);
     sp->cnt = static_cast<int*>(cnt);
@@ -249,7 +269,7 @@ int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq,
     int rc = check_gemm_args(who, M, N, K);
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(c, 4) || !aligned(sc, 4) || !aligned(wsc_gm, 4))
-        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes)", who);
+        return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes, ws 4)", who);
     return run_gemm(who, gsum, c, wq, wsc_gm, xq, sc, M, N, K, as_stream(stream));
 }
 
@@ -324,8 +344,8 @@ int rt4_gemv_w4a8_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const fl
     if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a8_cfg", rows, N, K);
     if (rc) return rc;
-    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 16) || !aligned(ws, 2))
-        return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: misaligned pointer (wq and x need 16 bytes)");
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 16) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a8_cfg: misaligned pointer (wq and x need 16 bytes, ws 4)");
     rt4::GemvCfg c;
     if ((rc = gemv_cfg("rt4_gemv_w4a8_cfg", K, rows, N, groups_per_wave, waves, k_splits, row_blocks, &c)))
         return rc;
@@ -338,17 +358,17 @@ int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8: null pointer");
     int rc = check_gemv_shape("k_gemv_w4a8", rows, N, K);
     if (rc) return rc;
-    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
-        return fail(RT4_E_ARG, "k_gemv_w4a8: misaligned pointer (wq needs 16 bytes)");
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "k_gemv_w4a8: misaligned pointer (wq needs 16 bytes, ws 4)");
     rt4::GemvCfg c;
     if ((rc = default_cfg(rows, N, K, &c))) return rc;
     // Two launches, as the reference: the activation quantizer into library
     // scratch, then the GEMV.  (The fused one-launch form, rt4_gemv_w4a8_cfg,
     // re-quantizes the activations in every tile and measures slower.)
-    void *q = nullptr, *s = nullptr;
-    if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q))) return rc;
-    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s))) return rc;
     hipStream_t st = as_stream(stream);
+    void *q = nullptr, *s = nullptr;
+    if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q, st))) return rc;
+    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s, st))) return rc;
     hipError_t e = rt4::launch_quant_act_a8(static_cast<int8_t*>(q), static_cast<float*>(s), nullptr, x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a8 quant launch");
     return run_gemv("k_gemv_w4a8 launch", nullptr, y, wq, ws, static_cast<const int8_t*>(q),
@@ -414,8 +434,8 @@ int rt4_gemv_w4a4_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const 
     if (!y || !wq || !ws || !aq || !sa) return fail(RT4_E_ARG, "rt4_gemv_w4a4: null pointer");
     int rc = check_gemv_shape("rt4_gemv_w4a4", rows, N, K);
     if (rc) return rc;
-    if (!aligned(wq, 16) || !aligned(aq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 2))
-        return fail(RT4_E_ARG, "rt4_gemv_w4a4: misaligned pointer (wq and aq need 16 bytes)");
+    if (!aligned(wq, 16) || !aligned(aq, 16) || !aligned(y, 4) || !aligned(sa, 4) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a4: misaligned pointer (wq and aq need 16 bytes, ws 4)");
     rt4::GemvCfg c;
     if ((rc = gemv4_cfg("rt4_gemv_w4a4", rows, N, K, groups_per_wave, waves, k_splits, &c))) return rc;
     return run_gemv4("rt4_gemv_w4a4 launch", y, wq, ws, aq, sa, rows, N, K, c, as_stream(stream));
@@ -431,12 +451,12 @@ int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "k_gemv_w4a4: null pointer");
     int rc = check_gemv_shape("k_gemv_w4a4", rows, N, K);
     if (rc) return rc;
-    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 2))
-        return fail(RT4_E_ARG, "k_gemv_w4a4: misaligned pointer (wq needs 16 bytes)");
-    void *q = nullptr, *s = nullptr;
-    if ((rc = scratch(kSlotActQ, (size_t)rows * K / 2, &q))) return rc;
-    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 32) * sizeof(float), &s))) return rc;
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "k_gemv_w4a4: misaligned pointer (wq needs 16 bytes, ws 4)");
     hipStream_t st = as_stream(stream);
+    void *q = nullptr, *s = nullptr;
+    if ((rc = scratch(kSlotActQ, (size_t)rows * K / 2, &q, st))) return rc;
+    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 32) * sizeof(float), &s, st))) return rc;
     hipError_t e = rt4::launch_quant_act_a4(static_cast<uint32_t*>(q), static_cast<float*>(s), x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a4 quant launch");
     rt4::GemvCfg c;
@@ -459,9 +479,9 @@ int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint3
     // The same per-group integers as the reference's int4 x int4 contraction, from
     // the codes sign-extended to int8 (library scratch: the caller hands over no
     // buffer for them).
-    void* q = nullptr;
-    if ((rc = scratch(kSlotGemmA, (size_t)M * K, &q))) return rc;
     hipStream_t st = as_stream(stream);
+    void* q = nullptr;
+    if ((rc = scratch(kSlotGemmA, (size_t)M * K, &q, st))) return rc;
     hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), nullptr, aq, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4 code expansion");
     return run_gemm("k_gemm_i4 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), asc_gm, M, N, K, st);
@@ -495,9 +515,9 @@ int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, 
     // Recombine the digit planes into int8 codes q8 = 16h + l.  The caller's c2
     // (M*N floats of scratch, src/k_gemm.hip:31) holds them when large enough.
     const size_t need = (size_t)M * K;
-    void* q = c2;
-    if ((size_t)M * N * sizeof(float) < need && (rc = scratch(kSlotGemmA, need, &q))) return rc;
     hipStream_t st = as_stream(stream);
+    void* q = c2;
+    if ((size_t)M * N * sizeof(float) < need && (rc = scratch(kSlotGemmA, need, &q, st))) return rc;
     hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4_a8 digit recombination");
     return run_gemm("k_gemm_i4_a8 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), sc, M, N, K, st);
@@ -559,11 +579,18 @@ int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, 
         return fail(RT4_E_ARG, "k_attention: misaligned pointer (qq, kc, out need 16 bytes)");
     int cus = 0, rc = device_cus(&cus);
     if (rc) return rc;
-    const int nsplit = kv_splits > 0 ? kv_splits : rt4::fa_splits(n_q, n_heads, n_tile, cus);
+    hipStream_t st = as_stream(stream);
+    int nsplit = kv_splits > 0 ? kv_splits : rt4::fa_splits(n_q, n_heads, n_tile, cus);
+    // Under graph capture an automatic split count that would need a larger
+    // workspace falls back to one split (no workspace; same algorithm, the fp32
+    // sums of O and L in one order instead of a combine of partial ranges).
+    if (nsplit > 1 && kv_splits == 0 && capturing(st) &&
+        !scratch_has(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit)))
+        nsplit = 1;
     void* part = nullptr;
-    if (nsplit > 1 && (rc = scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part))) return rc;
+    if (nsplit > 1 && (rc = scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st))) return rc;
     return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
-                                          kv_cap, nsplit, static_cast<float*>(part), as_stream(stream)),
+                                          kv_cap, nsplit, static_cast<float*>(part), st),
                       "k_attention launch");
 }
 

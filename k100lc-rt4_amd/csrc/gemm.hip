@@ -340,10 +340,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         mma(accB, a0, bu[1]);                       // tile (0,1)
         fold(facc[0][0], accA, ls, 0, 0, x);
         // the DMA of unit i+1 has landed once at most the 2 younger units' loads are pending;
-        // every wave has finished reading stage i (its LDS reads retire before the barrier)
-        // C stores of a tile flushed at the end of the previous unit are younger than the
-        // DMA awaited here; vmcnt retires in order, so a bound of 63 still covers that DMA
-        if (flushed) asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+        // every wave has finished reading stage i (its LDS reads retire before the barrier).
+        // After a flush the C stores of the previous tile are younger than that DMA and
+        // their number depends on how many rows and columns of the tile exist (stores to
+        // absent ones are never issued), so no count bound is safe: drain everything.
+        if (flushed) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
         flushed = false;
         __syncthreads();

@@ -2,12 +2,12 @@
 // prefill kernel (fa_int4, kernels/flash_attn_core.h:74-435), compiled in place
 // from /root/reference for gfx950 by oracle/Makefile into oracle/_ref/libref_hip.so.
 //
-// TEST INFRASTRUCTURE ONLY: tests/ run it on the same seeded inputs as a
-// third-party check of the CPU oracle's algorithm model and of our kernel.  Its
-// integer dot products are `v_dot8_i32_i4` inline assembly (flash_attn_core.h:61-64),
-// which gfx950 also implements; whether the gfx950 build computes the
-// reference's results is itself checked against the CPU oracle by the test
-// before the build is used as a reference.
+// TEST INFRASTRUCTURE ONLY: tests/test_attention.py runs it on the same seeded
+// quantized caches as our kernel (test_attention_against_reference_kernel, and the
+// full configs[4] shape).  Its integer dot products are `v_dot8_i32_i4` inline
+// assembly (flash_attn_core.h:61-64), which gfx950 implements with the same signed
+// int4 semantics; the tests first check this build against the CPU algorithm model
+// (rt4o_fa_rows mode 1) and then our kernel against this build.
 #include <hip/hip_runtime.h>
 #include <cstdint>
 typedef uint32_t u32;

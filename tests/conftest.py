@@ -56,7 +56,8 @@ def ref_hip(torch_gpu):
     L.ref_quant_rows.argtypes = [P, P, P, I, I, I, I, I]
     L.ref_quant_act4.argtypes = [P, P, P, I, I]
     L.ref_sync.argtypes = []
-    for f in ("ref_quant_act", "ref_quant_rows_a8", "ref_quant_rows", "ref_quant_act4", "ref_sync"):
+    L.ref_fa_int4.argtypes = [P] * 7 + [I] * 7
+    for f in ("ref_quant_act", "ref_quant_rows_a8", "ref_quant_rows", "ref_quant_act4", "ref_sync", "ref_fa_int4"):
         getattr(L, f).restype = None
     return L
 

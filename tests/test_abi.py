@@ -118,3 +118,30 @@ def test_single_hip_runtime_in_process(rt4):
     rt4.lib()
     maps = {line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line}
     assert len(maps) == 1, maps
+
+
+def test_gemv_scale_pointer_needs_4_bytes(rt4):
+    """The GEMVs load fp16 scale pairs as dwords (every row of an even-K/128 scale
+    matrix starts 4-byte aligned), so ws must be 4-byte aligned."""
+    L = rt4.lib()
+    W16, WS2 = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1002)
+    assert L.rt4_gemv_w4a8_q(W16, W16, WS2, W16, W16, 4, 64, 256, None) == 2
+    assert "ws 4" in L.rt4_last_error().decode()
+    assert L.rt4_gemv_w4a8(W16, W16, WS2, W16, 4, 64, 256, None) == 2
+    assert L.rt4_gemv_w4a8_cfg(W16, W16, WS2, W16, 4, 64, 256, 0, 0, 0, 0, None) == 2
+    assert L.rt4_gemv_w4a8_groupsums(W16, W16, W16, WS2, W16, W16, 4, 64, 256, None) == 2
+    assert L.rt4_gemv_w4a4_q(W16, W16, WS2, W16, W16, 4, 64, 256, None) == 2
+    assert L.rt4_gemv_w4a4(W16, W16, WS2, W16, 4, 64, 256, None) == 2
+
+
+@pytest.mark.parametrize("M,N,K", [(838861, 64, 5120), (128, 1677722, 5120), (128, 65536, 131072)])
+def test_gemm_rejects_shapes_beyond_32bit_offsets(rt4, M, N, K):
+    """The GEMM addresses rows of A (M*K bytes) and of W (N*K/2 bytes) with 32-bit
+    offsets; larger operands are rejected instead of wrapping."""
+    L = rt4.lib()
+    W16 = ctypes.c_void_p(0x1000)
+    assert L.rt4_gemm_w4a8_i8(W16, W16, W16, W16, W16, M, N, K, None) == 1
+    assert "32-bit offset" in L.rt4_last_error().decode()
+    assert L.rt4_gemm_w4a8_groupsums(W16, W16, W16, W16, W16, W16, M, N, K, None) == 1
+    # the largest operands inside the range still pass the shape check (fail later on alignment)
+    assert L.rt4_gemm_w4a8_i8(W16, ctypes.c_void_p(0x1004), W16, W16, W16, 838860, 64, 5120, None) == 2

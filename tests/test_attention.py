@@ -460,3 +460,84 @@ def test_graph_keeps_workspace_when_scratch_grows(rt4, torch_gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert np.array_equal(host(out).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,n_kv,off,H,KVH,cap,scale", [
+    (64, 320, 256, 2, 1, 320, True),       # the verdict's small shape: 5 whole tiles
+    (64, 320, 256, 2, 1, 320, False),      # unscaled Q: sharp softmax, the running max moves
+    (128, 300, 172, 6, 2, 320, True),      # GQA 3, ragged n_kv (partial 8-key V group)
+    (192, 1000, 808, 6, 1, 1024, True),    # GQA 6, partial last tile
+])
+def test_attention_against_reference_kernel(rt4, orc, torch_gpu, ref_hip, T, n_kv, off, H, KVH, cap, scale):
+    """The reference's own fa_int4 (kernels/flash_attn_core.h:74-435, launched as
+    src/k_fa.hip:294-296), built for gfx950 from its source, on the same quantized
+    cache: first against the CPU algorithm model (pins the model: tile max vs running
+    max, alpha/beta, P rounding), then our kernel against it."""
+    import ctypes
+    torch = torch_gpu
+    print(f"case attention vs reference fa_int4 T={T} n_kv={n_kv} off={off} H={H} KVH={KVH}", flush=True)
+    ref_hip.ref_fa_int4.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int] * 7
+    ref_hip.ref_fa_int4.restype = None
+    rng = np.random.default_rng(29)
+    q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    if not scale:
+        q = q * np.float32(16.0)
+    ratio = H // KVH
+    TP = (T + 63) // 64 * 64
+    g = gpu_cache(rt4, torch, q, k, v, TP, cap)
+    n_tile = (n_kv + BN - 1) // BN
+    ref_out = torch.zeros((H, TP, HD), dtype=torch.float32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    torch.cuda.synchronize()
+    ref_hip.ref_fa_int4(P(g[0]), P(g[1]), P(g[2]), P(g[3]), P(g[4]), P(g[5]), P(ref_out), T, n_kv, off, n_tile,
+                        H, ratio, cap)
+    ref_hip.ref_sync()
+    ours = host(rt4.attention_prefill(*g[:6], n_kv=n_kv, off=off, ratio=ratio))
+    torch.cuda.synchronize()
+    ref_o = host(ref_out)
+    c = [host(t).view(np.uint32) if t.dtype == torch.int32 else host(t) for t in g[:6]]
+    rows = np.arange(T, dtype=np.int32)
+    for h in range(H):
+        alg = orc.fa_rows(*c, TP, n_kv, off, cap, ratio, h, rows, 1)
+        e_model = rel_l2(ref_o[h, :T], alg)
+        e_ours = rel_l2(ours[h, :T], ref_o[h, :T])
+        print(f"  head {h}: reference kernel vs algorithm model {e_model:.2e}; ours vs reference kernel {e_ours:.2e}")
+        assert e_model < 1e-4
+        assert e_ours < 1e-4
+
+
+@pytest.mark.gpu
+def test_attention_benchmark_shape_against_reference_kernel(rt4, orc, torch_gpu, ref_hip):
+    """configs[4] in full: every output of our kernel against the reference's fa_int4
+    (built for gfx950) on the same quantized cache, plus sampled rows of the reference
+    kernel against the CPU algorithm model."""
+    import ctypes
+    torch = torch_gpu
+    c4 = workload.ATTN_C4
+    n_q, ctx, H, KVH = c4["n_q"], c4["ctx"], c4["H"], c4["KVH"]
+    n_kv = ctx + n_q
+    ratio = H // KVH
+    print(f"case attention C4 vs reference fa_int4 n_q={n_q} n_kv={n_kv}", flush=True)
+    rng = np.random.default_rng(31)
+    q, k, v = workload.attn_np(rng, n_q, n_kv, H, KVH)
+    g = gpu_cache(rt4, torch, q, k, v, n_q, n_kv)
+    ref_out = torch.zeros((H, n_q, HD), dtype=torch.float32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    torch.cuda.synchronize()
+    ref_hip.ref_fa_int4(P(g[0]), P(g[1]), P(g[2]), P(g[3]), P(g[4]), P(g[5]), P(ref_out), n_q, n_kv, ctx,
+                        n_kv // BN, H, ratio, n_kv)
+    ref_hip.ref_sync()
+    ours = rt4.attention_prefill(*g[:6], n_kv=n_kv, off=ctx, ratio=ratio)
+    torch.cuda.synchronize()
+    e_all = float((ours.double() - ref_out.double()).norm() / ref_out.double().norm())
+    print(f"  all {H}x{n_q}x{HD} outputs: ours vs reference kernel {e_all:.2e}")
+    assert e_all < 1e-4
+    ref_o = host(ref_out)
+    c = [host(t).view(np.uint32) if t.dtype == torch.int32 else host(t) for t in g[:6]]
+    rows = np.array([0, 63, 64, 700, 1023], np.int32)
+    for h in (0, 11, 23):
+        alg = orc.fa_rows(*c, n_q, n_kv, ctx, n_kv, ratio, h, rows, 1)
+        e = rel_l2(ref_o[h, rows], alg)
+        print(f"  head {h}: reference kernel vs algorithm model {e:.2e}")
+        assert e < 1e-4

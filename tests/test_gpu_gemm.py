@@ -121,3 +121,44 @@ def test_gemm_repeat_shapes(rt4, orc, torch_gpu):
         ni = rng.integers(0, N, 2048).astype(np.int32)
         ref, _ = _oracle_points(orc, c, M, N, K, mi, ni)
         assert rel_l2(host(y)[mi, ni], ref) < TIGHT
+
+
+@pytest.mark.parametrize("entry,M,N,K", [
+    ("i8", 1000, 17408, 5120),     # the reference's own prefill shape (docs/FORMAT.md:129)
+    ("dropin", 1024, 5184, 5120),  # N % 256 == 64: every column block ends in a partial tile
+    ("i8", 1000, 8320, 1024),      # M and N tails, 264 tiles: workgroups run on past whole tail tiles
+])
+def test_gemm_tail_tiles_with_continuing_workgroups(rt4, orc, torch_gpu, entry, M, N, K):
+    """Shapes whose workgroups own whole partial tiles (rows beyond M, columns beyond N)
+    and then continue with the next tile: the next tile's operands must have landed
+    whatever number of C stores the partial tile issued.  Sampled outputs against the
+    fp64 oracle; a second call is bitwise equal to the first."""
+    print(f"case gemm tails entry={entry} M={M} N={N} K={K}", flush=True)
+    c, wq, ws, x = _case(torch_gpu, 31, M, N, K)
+    sb = rt4.make_group_major(ws, K)
+    if entry == "i8":
+        xq, sc8 = rt4.quant_rows_i8(x)
+        run = lambda: rt4.gemm_w4a8_i8(wq, sb, xq, sc8)  # noqa: E731
+    else:
+        qh, ql, sc, sc16 = rt4.quant_rows_a8(x)
+        run = lambda: rt4.gemm_w4a8(wq, sb, qh, ql, sc, sc16)  # noqa: E731
+    y1 = host(run())
+    y2 = host(run())
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), "repeated call differs"
+    rng = np.random.default_rng(7)
+    P = 6144
+    mi = rng.integers(0, M, P).astype(np.int32)
+    ni = rng.integers(0, N, P).astype(np.int32)
+    # every corner, and rows / columns of the last partial tiles
+    m_t, n_t = min((M // 128) * 128, M - 1), min((N // 256) * 256, N - 1)
+    mi[:8] = [0, M - 1, 0, M - 1, M - 1, M - 2, m_t, M - 1]
+    ni[:8] = [0, 0, N - 1, N - 1, n_t, N - 1, N - 1, max(n_t - 1, 0)]
+    tail = rng.integers(0, P, 1024)
+    mi[tail] = rng.integers((M - 1) // 128 * 128, M, 1024)
+    ref, _ = _oracle_points(orc, c, M, N, K, mi, ni)
+    got = y1[mi, ni]
+    err = rel_l2(got, ref)
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    worst = float(np.abs(got - ref).max()) / rms
+    print(f"  rel_l2 = {err:.3e}  worst/rms = {worst:.3e}")
+    assert err < TIGHT and worst < 1e-5
