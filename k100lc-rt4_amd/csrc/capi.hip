@@ -114,6 +114,7 @@ int check_gemm_args(const char* who, int M, int N, int K) {
     if (M < 1 || N < 1) return fail(RT4_E_SHAPE, "%s: M=%d N=%d must be positive", who, M, N);
     if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "%s: K=%d is not a positive multiple of 128", who, K);
     if (M > 65535 * 128) return fail(RT4_E_SHAPE, "%s: M=%d too large", who, M);
+    if (N >= (1 << 23)) return fail(RT4_E_SHAPE, "%s: N=%d too large (at most 2^23 - 1 columns)", who, N);
     // the kernels address a row block of A and of W with 32-bit byte offsets
     if ((unsigned long long)M * (unsigned long long)K >= (1ull << 32) ||
         (unsigned long long)N * (unsigned long long)(K / 2) >= (1ull << 32))

@@ -13,45 +13,47 @@
 // 16*I_h + I_l = I exactly, so here the digits are recombined into int8 once
 // and a single int8 contraction runs on v_mfma_i32_32x32x32_i8.
 //
-// Tiling.  Workgroup tile 128 activation rows x 256 weight rows, 8 waves, each
-// wave a 64 x 64 block = 2 x 2 MFMA tiles of 32 x 32; one 128-wide K group is
-// four MFMA k-steps.  The int32 accumulators restart at every group (srcC = 0)
-// and are folded into fp32 with one fma per output:
-//     facc += f32(acc) * (sa * sb),   acc = 16*I exactly (x16 nibble unpack),
+// Tiling.  Workgroup tile 128 activation rows x 256 weight rows, 8 waves; wave w
+// owns weight rows (output columns) 32w..32w+31 and all 128 activation rows, i.e.
+// four 32 x 32 row tiles sharing one weight fragment, so each wave unpacks only
+// its own 32 weight rows.  One 128-wide K group ("unit" = one tile x one group)
+// is four MFMA k-steps per row tile.  The int32 accumulators restart at every
+// group and are folded into fp32:
+//     facc += f32(acc) * S,   S = sa * sb,   acc = 16*I exactly (x16 nibble unpack),
 // and the result is scaled by 1/16 once at the end (a power of two, so the bits
-// equal those of scaling every term).
+// equal those of scaling every term).  S is formed on the matrix core: one
+// v_mfma_f32_32x32x1_2b_f32 per pair of row tiles gives the rank-1 products
+// sa (x) sb in the accumulator layout, each a single fp32 product rounded once.
 //
-// Data movement.  Per group the workgroup moves 16 KB of int8 activations, 16 KB
+// What bounds this kernel on gfx950 is instruction issue: a SIMD issues about one
+// instruction per 4 cycles whatever its kind (scalar, vector, LDS, MFMA issue),
+// and the fold alone is two vector instructions per output per group.  So the
+// loop is built for few instructions: it is unrolled over the four LDS stages so
+// that every LDS address is a per-lane register plus an immediate offset; the DMA
+// sources are per-lane offsets (fixed while the tile is unchanged) plus scalar
+// base pointers advanced by a constant per unit; tile bookkeeping is a few
+// scalar counters.  The MFMAs of a row tile are interleaved one by one with the
+// fold of the previous row tile (and with the unpack of the next k-step), in an
+// order the compiler may not change (sched_barrier), so the matrix core and the
+// vector ALU work at the same time and no fold waits for the MFMA just issued.
+//
+// Data movement.  Per unit the workgroup moves 16 KB of int8 activations, 16 KB
 // of packed weights and the two scale vectors from global memory straight into
-// LDS with global_load_lds_dwordx4 (no VGPR round trip): four A+B stages and a
-// ring of five scale slots, so unit i+4 is loading while unit i computes.  The
-// LDS layouts are XOR-swizzled for gfx950's 64-bank LDS, which serves 16 lanes
-// of a ds_read_b128 per cycle: any 16 consecutive fragment rows hit 16 distinct
-// 16-byte bank groups.  The weights stay packed in LDS and are unpacked after
-// the ds_read.  The DMA is issued from inline asm with a per-lane 32-bit offset
-// (fixed while the tile is unchanged) and a scalar 64-bit base (advanced per
-// group), so it costs no vector ALU work; the compiler does not see it, so it
-// does not serialise LDS reads behind it -- the kernel waits itself (s_waitcnt
-// vmcnt + barrier).
+// LDS with global_load_lds_dwordx4 (no VGPR round trip), four stages deep (the
+// unit three ahead is loading while a unit computes).  Each wave loads exactly
+// the weight rows it reads; the activation tile is shared by all waves (one
+// barrier per unit).  LDS layouts are XOR-swizzled for gfx950's 64-bank LDS: any
+// 16 consecutive fragment rows of a ds_read_b128 hit 16 distinct 16-byte bank
+// groups.
 //
-// Per unit each wave: unpacks the weight fragments of the unit (read during the
-// previous unit), reads its second activation fragment, runs tiles (0,0) and
-// (0,1), folds (0,0), passes the one barrier of the unit (DMA of unit i+1 landed,
-// stage i free), issues the DMA of unit i+4 into stage i, reads the fragments of
-// unit i+1, and runs tiles (1,0), (1,1) with the remaining folds in between.
-// The fold (cvt + mul + fma per output per group) is most of the vector ALU
-// work, and on gfx950 vector ALU and MFMA issue overlap only a little, so the
-// kernel is bound by VALU + MFMA issue rather than by memory.
-//
-// Scheduling ("stream-K").  With 128 x 256 tiles the 27B shapes give 544 or 160
-// tiles for 256 CUs, so a plain one-tile-per-workgroup grid would leave up to
-// 30-40% of the machine idle in the last round.  Instead one persistent
-// workgroup per CU takes an equal, contiguous share of the (tile, group) units.
-// A tile split between workgroups is combined deterministically: every
-// contributor except the last writes its fp32 partial to a workspace slot
-// (agent-coherent stores), bumps the tile's counter, and the contributor that
-// arrives last sums all partials in workgroup order and writes C; it also resets
-// the counter for the next call.  No workgroup ever waits for another.
+// Scheduling ("stream-K").  One persistent workgroup per CU takes an equal,
+// contiguous share of the (tile, group) units, numbered so each XCD owns a
+// contiguous slice.  A tile split between workgroups is combined
+// deterministically: every contributor except the last writes its fp32 partial
+// to a workspace slot (agent-coherent stores), bumps the tile's counter, and the
+// contributor that arrives last sums all partials in workgroup order and writes
+// C; it also resets the counter for the next call.  No workgroup ever waits for
+// another.
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -59,157 +61,123 @@ namespace rt4 {
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;           // activation rows per tile
 constexpr int BN = 256;           // weight rows (output columns) per tile
 constexpr int NT = 512;           // 8 waves
+constexpr int NS = 4;             // LDS stages
 constexpr int A_ST = BM * 128;    // int8 activation tile per stage
 constexpr int B_ST = BN * 64;     // packed weight tile per stage
-constexpr int S_ST = 2048;        // sa (512 B) + sb (1024 B) + 512 B of the idle waves' loads
-constexpr int AB_ST = A_ST + B_ST;    // one A+B stage
-constexpr int NSC = 5;                // scale slots (a ring: unit i+4 is loaded while unit i folds)
-constexpr int DMA_PER_UNIT = 5;   // DMA instructions per wave per (tile, group) unit
+constexpr int S_ST = 2048;        // sa (512 B) + sb (1024 B) + 512 B written by the two idle waves
+constexpr int LDS_B = 0;                       // weight stages
+constexpr int LDS_A = LDS_B + NS * B_ST;       // activation stages
+constexpr int LDS_S = LDS_A + NS * A_ST;       // scale stages
+constexpr int LDS_FLAG = LDS_S + NS * S_ST;
+constexpr int LDS_META = LDS_FLAG + 16;            // split-tile metadata (10 ints)
+constexpr int LDS_BYTES = LDS_META + 48;
+constexpr int DMA_PER_UNIT = 5;   // DMA instructions per wave per unit
 constexpr int PART_FLOATS = NT * 64;   // one partial tile: 64 outputs per thread, [k][thread]
 
 __device__ __forceinline__ uint32_t lds_addr(const unsigned char* l) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(lds_void*)l);
 }
-// global -> LDS, 16 (resp. 4) bytes per lane; lane i lands at m0 + 16*i (4*i).
-__device__ __forceinline__ void dma16(const void* g, unsigned char* l) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(l)) : "memory");
+// A wave-uniform pointer as a scalar register pair.
+__device__ __forceinline__ const void* sptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const void*>((uintptr_t)(((uint64_t)hi << 32) | lo));
 }
-__device__ __forceinline__ void dma4(const void* g, unsigned char* l) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(l)) : "memory");
+// global -> LDS: lane i's 16 (4) bytes at gbase + voff land at m0 + 16*i (4*i),
+// m0 = lbase + IMM.  The scalar base keeps the per-lane address a 32-bit offset.
+template <int IMM>
+__device__ __forceinline__ void dma16(uint32_t voff, const void* gbase, uint32_t lbase) {
+    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sptr(gbase)),
+                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
+                 : "memory");
+}
+template <int IMM>
+__device__ __forceinline__ void dma4(uint32_t voff, const void* gbase, uint32_t lbase) {
+    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sptr(gbase)),
+                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
+                 : "memory");
 }
 // Device-scope (sc1) 16-byte stores / loads of split-tile partials, the cache
 // policy of agent-scope atomics: the stores write through the per-XCD L2 and
 // are in memory once the writer's s_waitcnt has retired them, and the loads
-// read the coherent copy.
-typedef float v4f __attribute__((ext_vector_type(4)));
-// Eight device-scope 16-byte stores (one every NT*4 floats) and the wait for
-// them in one asm statement: store data VGPRs must not be overwritten before the
-// stores have read them, which the compiler cannot know for asm stores.
-__device__ __forceinline__ void store8_dev16(float* p, const v4f* v) {
+// read the coherent copy.  Four at a time (one row tile's 16 values per lane,
+// at a stride of NT*4 floats), each with its wait in the same asm statement:
+// store data registers must not be overwritten before the stores have read them,
+// and loaded registers must not be touched before they are valid, neither of
+// which the compiler can know for asm memory operations.
+__device__ __forceinline__ void store4_dev16(float* p, const v16i& f) {
     constexpr size_t S = (size_t)NT * 4;
+    const v4i v0 = __builtin_shufflevector(f, f, 0, 1, 2, 3), v1 = __builtin_shufflevector(f, f, 4, 5, 6, 7);
+    const v4i v2 = __builtin_shufflevector(f, f, 8, 9, 10, 11), v3 = __builtin_shufflevector(f, f, 12, 13, 14, 15);
     asm volatile(
-        "global_store_dwordx4 %0, %8, off sc1\n\t"
-        "global_store_dwordx4 %1, %9, off sc1\n\t"
-        "global_store_dwordx4 %2, %10, off sc1\n\t"
-        "global_store_dwordx4 %3, %11, off sc1\n\t"
-        "global_store_dwordx4 %4, %12, off sc1\n\t"
-        "global_store_dwordx4 %5, %13, off sc1\n\t"
-        "global_store_dwordx4 %6, %14, off sc1\n\t"
-        "global_store_dwordx4 %7, %15, off sc1\n\t"
+        "global_store_dwordx4 %0, %4, off sc1\n\t"
+        "global_store_dwordx4 %1, %5, off sc1\n\t"
+        "global_store_dwordx4 %2, %6, off sc1\n\t"
+        "global_store_dwordx4 %3, %7, off sc1\n\t"
         "s_waitcnt vmcnt(0) expcnt(0)"
         :
-        : "v"(p), "v"(p + S), "v"(p + 2 * S), "v"(p + 3 * S), "v"(p + 4 * S), "v"(p + 5 * S), "v"(p + 6 * S),
-          "v"(p + 7 * S), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7])
+        : "v"(p), "v"(p + S), "v"(p + 2 * S), "v"(p + 3 * S), "v"(v0), "v"(v1), "v"(v2), "v"(v3)
         : "memory");
 }
-// Eight such loads (one every NT*4 floats) and the wait for them in a single asm
-// statement, so the destination registers are not touched before they are valid.
-__device__ __forceinline__ void load8_dev16(v4f* v, const float* p) {
+__device__ __forceinline__ void add4_dev16(v16i& f, const float* p) {
     constexpr size_t S = (size_t)NT * 4;
+    v4f v0, v1, v2, v3;
     asm volatile(
-        "global_load_dwordx4 %0, %8, off sc1\n\t"
-        "global_load_dwordx4 %1, %9, off sc1\n\t"
-        "global_load_dwordx4 %2, %10, off sc1\n\t"
-        "global_load_dwordx4 %3, %11, off sc1\n\t"
-        "global_load_dwordx4 %4, %12, off sc1\n\t"
-        "global_load_dwordx4 %5, %13, off sc1\n\t"
-        "global_load_dwordx4 %6, %14, off sc1\n\t"
-        "global_load_dwordx4 %7, %15, off sc1\n\t"
+        "global_load_dwordx4 %0, %4, off sc1\n\t"
+        "global_load_dwordx4 %1, %5, off sc1\n\t"
+        "global_load_dwordx4 %2, %6, off sc1\n\t"
+        "global_load_dwordx4 %3, %7, off sc1\n\t"
         "s_waitcnt vmcnt(0)"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
-        : "v"(p), "v"(p + S), "v"(p + 2 * S), "v"(p + 3 * S), "v"(p + 4 * S), "v"(p + 5 * S), "v"(p + 6 * S),
-          "v"(p + 7 * S)
+        : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
+        : "v"(p), "v"(p + S), "v"(p + 2 * S), "v"(p + 3 * S)
         : "memory");
-}
-
-struct Unit {
-    int t, g, tm, tn;
-    __device__ __forceinline__ int bm() const { return tm * BM; }
-    __device__ __forceinline__ int bn() const { return tn * BN; }
-    __device__ __forceinline__ void next(int NG, int ntm) {
-        if (++g == NG) {
-            g = 0;
-            ++t;
-            if (++tm == ntm) {
-                tm = 0;
-                ++tn;
-            }
-        }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = __float_as_int(__int_as_float(f[e]) + v0[e]);
+        f[4 + e] = __float_as_int(__int_as_float(f[4 + e]) + v1[e]);
+        f[8 + e] = __float_as_int(__int_as_float(f[8 + e]) + v2[e]);
+        f[12 + e] = __float_as_int(__int_as_float(f[12 + e]) + v3[e]);
     }
-};
-
-__device__ __forceinline__ Unit unit_of(int u, int NG, int ntm) {
-    Unit x;
-    x.t = u / NG;
-    x.g = u - x.t * NG;
-    x.tn = x.t / ntm;                 // consecutive tiles share their weight rows
-    x.tm = x.t - x.tn * ntm;
-    return x;
 }
 
-// The DMA of one unit: per wave 2 A instructions (8 rows x 128 B each), 2 B
-// instructions (16 rows x 64 B each) and 1 scale instruction.  LDS layouts:
-//   A  [128 rows][8 x 16 B], 16-byte chunk c of row r stored at c ^ ((r >> 1) & 7)
-//   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3)
-//   S  sa[128] f32, sb[256] f32
-// Per-lane byte offsets of this wave's DMA sources within one (tile, group) unit,
-// relative to the unit's scalar bases; they change only when the tile changes.
+// Per-lane byte offsets of this wave's DMA sources for one tile (relative to the
+// unit's scalar bases), unchanged while the tile is.  LDS layouts:
+//   A  [128 rows][8 x 16 B], 16-byte chunk c of row r stored at c ^ ((r >> 1) & 7);
+//      wave w loads rows 16w..16w+15 (two instructions of 8 rows x 128 B)
+//   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3);
+//      wave w loads rows 32w..32w+31, the ones it reads
+//   S  sa[128] f32 (waves 0, 1), sb[256] f32 (waves 2..5); waves 6, 7 repeat an sb
+//      load into the spare 512 B so that every wave issues the same count.
 struct DmaOff {
     uint32_t a[2], b[2], s;
 };
-__device__ __forceinline__ DmaOff dma_offsets(const Unit& x, int M, int N, int K, int w, int lane) {
+__device__ __forceinline__ DmaOff dma_offsets(int bm, int bn, int M, int N, int K, int w, int lane) {
     DmaOff o;
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        const int i = 2 * w + t;
-        const int r = 8 * i + (lane >> 3);
+        const int r = 16 * w + 8 * t + (lane >> 3);
         const int c = (lane & 7) ^ ((r >> 1) & 7);
-        int gr = x.bm() + r;
-        gr = gr < M ? gr : M - 1;
+        const int gr = min(bm + r, M - 1);
         o.a[t] = (uint32_t)gr * (uint32_t)K + c * 16;
     }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
-        const int i = 2 * w + t;
-        const int r = 16 * i + (lane >> 2);
+        const int r = 32 * w + 16 * t + (lane >> 2);
         const int c = (lane & 3) ^ ((r >> 2) & 3);
-        int gr = x.bn() + r;
-        gr = gr < N ? gr : N - 1;
+        const int gr = min(bn + r, N - 1);
         o.b[t] = (uint32_t)gr * (uint32_t)(K >> 1) + c * 16;
     }
-    if (w < 2) {
-        int r = x.bm() + w * 64 + lane;
-        o.s = (uint32_t)(r < M ? r : M - 1) * 4u;
-    } else {
-        int r = x.bn() + ((w - 2) & 3) * 64 + lane;
-        o.s = (uint32_t)(r < N ? r : N - 1) * 4u;
-    }
-    return o;
-}
-__device__ __forceinline__ void dma16s(uint32_t voff, const void* base, unsigned char* l) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds_addr(l)) : "memory");
-}
-__device__ __forceinline__ void dma4s(uint32_t voff, const void* base, unsigned char* l) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds_addr(l)) : "memory");
-}
-__device__ __forceinline__ void issue(unsigned char* st, unsigned char* sdst, const int8_t* __restrict__ A,
-                                      const uint32_t* __restrict__ W, const float* __restrict__ sa,
-                                      const float* __restrict__ sb, int M, int N, int K, const Unit& x,
-                                      const DmaOff& o, int w) {
-    const int8_t* ab = A + (size_t)x.g * 128;
-    const unsigned char* wb = reinterpret_cast<const unsigned char*>(W) + (size_t)x.g * 64;
-    dma16s(o.a[0], ab, st + (2 * w) * 1024);
-    dma16s(o.a[1], ab, st + (2 * w + 1) * 1024);
-    dma16s(o.b[0], wb, st + A_ST + (2 * w) * 1024);
-    dma16s(o.b[1], wb, st + A_ST + (2 * w + 1) * 1024);
     if (w < 2)
-        dma4s(o.s, sa + (size_t)x.g * M, sdst + w * 256);
+        o.s = (uint32_t)min(bm + 64 * w + lane, M - 1) * 4u;
     else
-        dma4s(o.s, sb + (size_t)x.g * N, sdst + 512 + (w < 6 ? 0 : 1024) + ((w - 2) & 3) * 256);
+        o.s = (uint32_t)min(bn + 64 * ((w - 2) & 3) + lane, N - 1) * 4u;
+    return o;
 }
 
 // Which workgroup's share contains unit u (shares are [T*b/P, T*(b+1)/P)).
@@ -217,6 +185,10 @@ __device__ __forceinline__ int owner_of(long long u, long long T, int P) {
     return (int)(((u + 1) * P - 1) / T);
 }
 
+// Tile coordinates of a unit, as the flush and the group-sum stores need them.
+struct TileRef {
+    int t, bm, bn, g;
+};
 
 template <bool GSUM>
 __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ A,
@@ -228,12 +200,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
                                                      float* __restrict__ part,
                                                      int* __restrict__ cnt, int M, int N, int K,
                                                      int ntm, long long T) {
-    __shared__ __align__(16) unsigned char sab[4 * AB_ST];
-    __shared__ __align__(16) unsigned char ssc[NSC * S_ST];
-    __shared__ int s_flag;
+    __shared__ __align__(16) unsigned char lds[LDS_BYTES];
+    int* s_flag = reinterpret_cast<int*>(lds + LDS_FLAG);
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6);
-    const int wm = w & 1, wn = w >> 1;
     const int lr = lane & 31, lh = lane >> 5;
     const int NG = K >> 7;
     const int P = gridDim.x;
@@ -242,201 +212,350 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     const int n = (int)(u1 - u0);
     const int first_tile = (int)(u0 / NG);
 
-    v16i facc[2][2];
+    // per-lane LDS read offsets; stage, row tile and pair are immediates
+    int ra[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int ks = 0; ks < 4; ks++) ra[ks] = LDS_A + lr * 128 + (((4 * (ks >> 1) + 2 * lh + (ks & 1)) ^ ((lr >> 1) & 7)) * 16);
+    int rb[2];
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) facc[i][j][r] = 0;
+    for (int s2 = 0; s2 < 2; s2++) {
+        const int r = 32 * w + lr;
+        rb[s2] = LDS_B + r * 64 + (((2 * s2 + lh) ^ ((r >> 2) & 3)) * 16);
+    }
+    int rsa = LDS_S + lr * 4, rsb = LDS_S + 512 + (32 * w + lr) * 4;
+    // per-wave LDS destinations of the DMA (m0 = base + stage immediate)
+    const uint32_t L = lds_addr(lds);
+    const uint32_t dstA = L + LDS_A + 2 * w * 1024, dstB = L + LDS_B + 2 * w * 1024;
+    const uint32_t dstS = L + LDS_S + (w < 2 ? w * 256 : w < 6 ? 512 + (w - 2) * 256 : 1536);
 
-    auto stage = [&](int i) { return sab + (i & 3) * AB_ST; };
-    auto slot = [&](int i) { return ssc + (i % NSC) * S_ST; };
-    auto read_a = [&](v4i (&dst)[4], const unsigned char* stg, int ii) {
-        const int r = 64 * wm + 32 * ii + lr;
+    // facc[ii]: row tile ii (rows 32 ii..32 ii+31) x this wave's 32 columns; lane (lr, lh)
+    // holds column 32w + lr, rows 32 ii + 8q + 4lh + e in register 4q + e.
+    v16i facc[4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int c = (4 * (ks >> 1) + 2 * lh + (ks & 1)) ^ ((r >> 1) & 7);
-            dst[ks] = *reinterpret_cast<const v4i*>(stg + r * 128 + c * 16);
-        }
-    };
-    auto read_b = [&](uint4 (&dst)[2][2], const unsigned char* stg) {
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int s2 = 0; s2 < 2; s2++) {
-                const int r = 64 * wn + 32 * j + lr;
-                const int c = (2 * s2 + lh) ^ ((r >> 2) & 3);
-                dst[j][s2] = *reinterpret_cast<const uint4*>(stg + A_ST + r * 64 + c * 16);
-            }
-    };
+        for (int r = 0; r < 16; r++) facc[i][r] = 0;
+
     const v16i zero16 = {};
-    auto mma = [&](v16i& acc, const v4i (&a)[4], const v4i (&bb)[4]) {
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], bb[0], zero16, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], bb[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[2], bb[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[3], bb[3], acc, 0, 0, 0);
+    const v16f zero16f = {};
+    auto unpack_ks = [&](v4i (&bu_)[4], const uint4 (&bp_)[2], int ks) {
+        const uint4 p = bp_[ks >> 1];
+        const uint32_t x0 = (ks & 1) ? p.z : p.x, x1 = (ks & 1) ? p.w : p.y;
+        bu_[ks] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
     };
-    // fold of tile (ii, j): lane holds column 32j + lr, rows 8q + 4lh + e
-    auto fold = [&](v16i& fa, const v16i& acc, const float* ls, int ii, int j, const Unit& x) {
-        const float sbv = ls[128 + 64 * wn + 32 * j + lr];
+    // Scale products of row tile ii on the matrix core: v_mfma_f32_32x32x2_f32 with
+    // A = [sa | 0] and B = [sb ; 0] (lanes 32..63 supply k = 1) gives
+    // S[r] = sa[row of register r] * sb[this lane's column] in the accumulator
+    // layout of the int8 tiles, each a single fp32 product rounded once (the bits of
+    // sa * sb on the vector ALU; the zero half adds +0 exactly).  One of the three
+    // fold operations per output thus leaves the vector ALU.
+    auto sa_of = [&](int ii) __attribute__((always_inline)) -> float {
+        const float a = *reinterpret_cast<const float*>(lds + rsa + ii * 128);
+        return lh ? 0.f : a;
+    };
+    auto scales = [&](float saz, float sbz) __attribute__((always_inline)) -> v16f {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(saz, sbz, zero16f, 0, 0, 0);
+    };
+    // quarter q of the fold of row tile ii (registers 4q..4q+3)
+    auto fold_q = [&](v16i& fa, const v16i& acc, const v16f& S, int ii, int q, const TileRef& x) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 v = *reinterpret_cast<const float4*>(ls + 64 * wm + 32 * ii + 8 * q + 4 * lh);
-            const float sv[4] = {v.x, v.y, v.z, v.w};
+        for (int r = 4 * q; r < 4 * q + 4; r++)
+            fa[r] = __float_as_int(fmaf((float)acc[r], S[r], __int_as_float(fa[r])));
+        if (GSUM && x.g >= 0) {
+            const int nn = x.bn + 32 * w + lr;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int r = 4 * q + e;
-                fa[r] = __float_as_int(fmaf((float)acc[r], sv[e] * sbv, __int_as_float(fa[r])));
-            }
-        }
-        if (GSUM) {
-            const int nn = x.bn() + 64 * wn + 32 * j + lr;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
+            for (int r = 4 * q; r < 4 * q + 4; r++) {
+                const int m = x.bm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (m < M && nn < N) gsum[((size_t)m * N + nn) * NG + x.g] = acc[r] >> 4;
             }
         }
     };
 
-    // prologue: DMA of units 0..3 (clamped to the last unit), then fragments of unit 0
-    Unit cu = unit_of((int)u0, NG, ntm);
-    Unit iu = cu;
-    DmaOff off = dma_offsets(iu, M, N, K, w, lane);
-    auto advance = [&]() {
-        iu.next(NG, ntm);
-        if (iu.g == 0) off = dma_offsets(iu, M, N, K, w, lane);
-    };
+    // End of this workgroup's segment of tile x.t: publish it (see the file comment).
+    // Split-tile metadata of this workgroup's first and last tile (only these can be
+    // shared with other workgroups), formed once here so that the flush, which runs
+    // amid the pipeline's live registers, needs no 64-bit arithmetic:
+    //   [0] first tile, [1] whole, [2] owner of its first unit, [3] owner of its last
+    //   unit, [4] partial slot of that first owner; [5..9] the same for the last tile.
+    // A contributor v writes its partial of tile t to slot 2v (t is v's first tile) or
+    // 2v + 1 (its last tile).  Every contributor after the first owner starts its
+    // share inside t, so t is its first tile; the first owner's slot is 0 only if its
+    // share starts exactly at the tile's first unit.
+    int* meta = reinterpret_cast<int*>(lds + LDS_META);
+    if (threadIdx.x == 0) {
+        const long long tl = (u1 - 1) / NG;
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        if (s > 0 && s < n) advance();
-        issue(stage(s), slot(s), A, W, sa, sb, M, N, K, iu, off, w);
-    }
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * DMA_PER_UNIT) : "memory");
-    __syncthreads();
-    v4i a0[4], a1[4];
-    uint4 bp[2][2];
-    read_a(a0, stage(0), 0);
-    read_b(bp, stage(0));
-
-    bool flushed = false;
-    for (int i = 0; i < n; i++) {
-        const Unit x = cu;
-        cu.next(NG, ntm);
-        const float* ls = reinterpret_cast<const float*>(slot(i));
-        v4i bu[2][4];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const uint4 p = bp[j][ks >> 1];
-                const uint32_t x0 = (ks & 1) ? p.z : p.x, x1 = (ks & 1) ? p.w : p.y;
-                bu[j][ks] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
-            }
-        read_a(a1, stage(i), 1);
-        v16i accA, accB;
-        mma(accA, a0, bu[0]);                       // tile (0,0)
-        mma(accB, a0, bu[1]);                       // tile (0,1)
-        fold(facc[0][0], accA, ls, 0, 0, x);
-        // the DMA of unit i+1 has landed once at most the 2 younger units' loads are pending;
-        // every wave has finished reading stage i (its LDS reads retire before the barrier).
-        // After a flush the C stores of the previous tile are younger than that DMA and
-        // their number depends on how many rows and columns of the tile exist (stores to
-        // absent ones are never issued), so no count bound is safe: drain everything.
-        if (flushed) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
-        flushed = false;
-        __syncthreads();
-        if (i + 4 < n) advance();
-        issue(stage(i), slot(i + 4), A, W, sa, sb, M, N, K, iu, off, w);
-        read_a(a0, stage(i + 1), 0);
-        read_b(bp, stage(i + 1));
-        mma(accA, a1, bu[0]);                       // tile (1,0)
-        fold(facc[0][1], accB, ls, 0, 1, x);
-        mma(accB, a1, bu[1]);                       // tile (1,1)
-        fold(facc[1][0], accA, ls, 1, 0, x);
-        fold(facc[1][1], accB, ls, 1, 1, x);
-
-        // --- end of this workgroup's segment of tile x.t: publish it
-        if (x.g == NG - 1 || i == n - 1) {
-            flushed = true;
-            const long long tb = (long long)x.t * NG, te = tb + NG;
-            bool write_c = true;
-            if (!(u0 <= tb && u1 >= te)) {
-                const int slt = (x.t == first_tile) ? 0 : 1;
-                float* my = part + ((size_t)b * 2 + slt) * PART_FLOATS + (size_t)threadIdx.x * 4;
-                v4f pv[16];
-#pragma unroll
-                for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-#pragma unroll
-                        for (int r4 = 0; r4 < 4; r4++)
-                            pv[(ii * 2 + j) * 4 + r4] = v4f{
-                                __int_as_float(facc[ii][j][4 * r4]), __int_as_float(facc[ii][j][4 * r4 + 1]),
-                                __int_as_float(facc[ii][j][4 * r4 + 2]), __int_as_float(facc[ii][j][4 * r4 + 3])};
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                store8_dev16(my, pv);
-                store8_dev16(my + (size_t)8 * NT * 4, pv + 8);
-                __syncthreads();
-                const int wf = owner_of(tb, T, P), wl = owner_of(te - 1, T, P);
-                if (threadIdx.x == 0)
-                    s_flag = __hip_atomic_fetch_add(cnt + x.t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                             wl - wf;
-                __syncthreads();
-                write_c = s_flag;
-                if (write_c) {
-#pragma unroll
-                    for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                        for (int j = 0; j < 2; j++)
-#pragma unroll
-                            for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
-                    for (int v = wf; v <= wl; v++) {
-                        const int ft = (int)((T * v / P) / NG);
-                        const float* pp = part + ((size_t)v * 2 + (ft == x.t ? 0 : 1)) * PART_FLOATS +
-                                          (size_t)threadIdx.x * 4;
-                        v4f pv2[16];
-                        load8_dev16(pv2, pp);
-                        load8_dev16(pv2 + 8, pp + (size_t)8 * NT * 4);
-#pragma unroll
-                        for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                            for (int j = 0; j < 2; j++)
-#pragma unroll
-                                for (int r = 0; r < 16; r++) {
-                                    const float f = __int_as_float(facc[ii][j][r]);
-                                    facc[ii][j][r] = __float_as_int(f + pv2[(ii * 2 + j) * 4 + (r >> 2)][r & 3]);
-                                }
-                    }
-                    if (threadIdx.x == 0)
-                        __hip_atomic_store(cnt + x.t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            if (write_c) {
-#pragma unroll
-                for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        const int nn = x.bn() + 64 * wn + 32 * j + lr;
-                        if (nn < N)
-#pragma unroll
-                            for (int r = 0; r < 16; r++) {
-                                const int m = x.bm() + 64 * wm + 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
-                                if (m < M) C[(size_t)m * N + nn] = __int_as_float(facc[ii][j][r]) * 0.0625f;
-                            }
-                    }
-            }
-#pragma unroll
-            for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) facc[ii][j][r] = 0;
+        for (int e = 0; e < 2; e++) {
+            const long long t = e ? tl : (long long)first_tile;
+            const long long tb = t * NG, te = tb + NG;
+            const int wf = owner_of(tb, T, P), wl = owner_of(te - 1, T, P);
+            meta[5 * e + 0] = (int)t;
+            meta[5 * e + 1] = (u0 <= tb && u1 >= te);
+            meta[5 * e + 2] = wf;
+            meta[5 * e + 3] = wl;
+            meta[5 * e + 4] = (T * wf / P == tb) ? 0 : 1;
         }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // drain the clamped tail DMA before exit
+
+    // End of this workgroup's segment of tile x.t: publish it (see the file comment).
+    auto flush = [&](const TileRef& x) __attribute__((always_inline)) {
+        // only the first and the last tile of a share can be split; tiles between are whole
+        const int tf = uniform(meta[0]), tl = uniform(meta[5]);
+        const int e = x.t == tf ? 0 : 5;
+        const bool whole = (x.t != tf && x.t != tl) || uniform(meta[e + 1]);
+        bool write_c = true;
+        if (!whole) {
+            const int wf = uniform(meta[e + 2]), wl = uniform(meta[e + 3]), slot_f = uniform(meta[e + 4]);
+            float* my = part + ((size_t)b * 2 + (e ? 1 : 0)) * PART_FLOATS + (size_t)threadIdx.x * 4;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) store4_dev16(my + (size_t)ii * 4 * NT * 4, facc[ii]);
+            __syncthreads();
+            if (threadIdx.x == 0)
+                *s_flag = __hip_atomic_fetch_add(cnt + x.t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == wl - wf;
+            __syncthreads();
+            write_c = *s_flag;
+            if (write_c) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) facc[ii][r] = 0;
+                for (int v = wf; v <= wl; v++) {
+                    const int slot = 2 * v + (v == wf ? slot_f : 0);
+                    const float* pp = part + (size_t)slot * PART_FLOATS + (size_t)threadIdx.x * 4;
+#pragma unroll
+                    for (int ii = 0; ii < 4; ii++) add4_dev16(facc[ii], pp + (size_t)ii * 4 * NT * 4);
+                }
+                if (threadIdx.x == 0) __hip_atomic_store(cnt + x.t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        if (write_c) {
+            // N passes through an empty asm: the row offsets below are then formed here,
+            // in this rare path, instead of being hoisted out of the loops into registers
+            // held for the whole kernel.
+            int Nv = N;
+            asm volatile("" : "+s"(Nv));
+            const uint32_t nn = (uint32_t)(x.bn + 32 * w + lr);
+            float* cb = C + (size_t)x.bm * Nv + nn;
+            const int mrows = M - x.bm;
+            if (nn < (uint32_t)N) {
+                if (mrows >= BM) {
+#pragma unroll
+                    for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int ml = 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
+                            cb[(size_t)ml * Nv] = __int_as_float(facc[ii][r]) * 0.0625f;
+                            __builtin_amdgcn_sched_barrier(0);   // one address at a time
+                        }
+                } else {
+#pragma unroll
+                    for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int ml = 32 * ii + 8 * (r >> 2) + 4 * lh + (r & 3);
+                            if (ml < mrows) cb[(size_t)ml * Nv] = __int_as_float(facc[ii][r]) * 0.0625f;
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                }
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) facc[ii][r] = 0;
+    };
+
+    // ---- DMA side: the unit being loaded.  Its sources are the kernel arguments
+    // (scalar bases) plus per-lane 32-bit offsets that hold the row, the chunk and
+    // the group: each unit adds one group to them, a new tile recomputes them.
+    int dleft, dtm, dtn, dg0;
+    {
+        const int t0 = (int)(u0 / NG);
+        dg0 = (int)(u0 - (long long)t0 * NG);
+        dleft = NG - dg0;
+        dtn = t0 / ntm;
+        dtm = t0 - dtn * ntm;
+    }
+    const void* sbase = (w < 2 ? (const void*)sa : (const void*)sb);
+    const uint32_t s_step = (w < 2 ? (uint32_t)M : (uint32_t)N) * 4u;
+    DmaOff off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
+    off.a[0] += dg0 * 128;
+    off.a[1] += dg0 * 128;
+    off.b[0] += dg0 * 64;
+    off.b[1] += dg0 * 64;
+    off.s += dg0 * s_step;
+    // DMA of the unit at the DMA side's position into stage st
+    auto issue = [&](int st) __attribute__((always_inline)) {
+        const uint32_t da = dstA + st * A_ST, db = dstB + st * B_ST, ds = dstS + st * S_ST;
+        dma16<0>(off.a[0], A, da);
+        dma16<1024>(off.a[1], A, da);
+        dma16<0>(off.b[0], W, db);
+        dma16<1024>(off.b[1], W, db);
+        dma4<0>(off.s, sbase, ds);
+    };
+    auto advance_dma = [&]() __attribute__((always_inline)) {
+        if (--dleft == 0) {
+            dleft = NG;
+            if (++dtm == ntm) {
+                dtm = 0;
+                ++dtn;
+            }
+            off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
+        } else {
+            off.a[0] += 128;
+            off.a[1] += 128;
+            off.b[0] += 64;
+            off.b[1] += 64;
+            off.s += s_step;
+        }
+    };
+
+    // ---- compute side: the tile of the current segment of units
+    TileRef cur;
+    {
+        const int t0 = (int)(u0 / NG);
+        cur.t = t0;
+        cur.g = (int)(u0 - (long long)t0 * NG);
+        const int tn = t0 / ntm;
+        cur.bm = (t0 - tn * ntm) * BM;
+        cur.bn = tn * BN;
+    }
+
+    // prologue: DMA of units 0..3, then the fragments of unit 0
+    issue(0);
+    if (n > 1) { advance_dma(); issue(1); }
+    if (n > 2) { advance_dma(); issue(2); }
+    if (n > 3) { advance_dma(); issue(3); }
+    if (n > 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * DMA_PER_UNIT) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    v4i a_cur[4], a_nxt[4], bu[4];
+    uint4 bp[2];
+    // fragment reads: per-lane offsets into the current stage (moved on by one stage
+    // per unit: one add per register) plus the row tile (an immediate)
+    auto next_stage = [&](int st_next) __attribute__((always_inline)) {
+        const int da = st_next ? A_ST : -(NS - 1) * A_ST, db = st_next ? B_ST : -(NS - 1) * B_ST;
+        const int ds = st_next ? S_ST : -(NS - 1) * S_ST;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) ra[ks] += da;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) rb[s2] += db;
+        rsa += ds;
+        rsb += ds;
+    };
+    auto read_a = [&](v4i (&dst)[4], int ii) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) dst[ks] = *reinterpret_cast<const v4i*>(lds + ra[ks] + ii * 4096);
+    };
+    auto read_b = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) bp[s2] = *reinterpret_cast<const uint4*>(lds + rb[s2]);
+    };
+    read_a(a_cur, 0);
+    read_b();
+
+    // Software pipeline over row tiles: the MFMAs of row tile t run while tile t-1
+    // is folded.  The last tile of a unit is folded during the first tile of the
+    // next unit of the same segment; at the end of a segment it is folded there and
+    // the segment is published.
+    // Accumulators with fixed roles: row tiles 0 and 2 of a unit go to accA, tiles
+    // 1 and 3 to accB, and a fold reads the one the MFMAs are not writing (no copies).
+    v16i accA, accB;
+    v16f S;              // scale products of the row tile being folded
+    // One row-tile step: the four MFMAs of tile (a, bu) into acc, each followed by a
+    // quarter of the fold of the previous tile (prev into facc[fi]) and, with
+    // UNPACK, by the unpack of the next k-step's weights; with LATE the fold starts
+    // one MFMA later (its scale products are still being formed).
+    auto step = [&](const v4i (&a)[4], v16i& acc, const v16i& prev, v16i& fa, int fi, const TileRef& fx,
+                    bool do_unpack, bool late) __attribute__((always_inline)) {
+        if (do_unpack) unpack_ks(bu, bp, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks], bu[ks], ks ? acc : zero16, 0, 0, 0);
+            if (do_unpack && ks < 3) unpack_ks(bu, bp, ks + 1);
+            if (!late) fold_q(fa, prev, S, fi, ks, fx);
+            else if (ks == 1) { fold_q(fa, prev, S, fi, 0, fx); fold_q(fa, prev, S, fi, 1, fx); }
+            else if (ks > 1) fold_q(fa, prev, S, fi, ks, fx);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // One unit (one group of the current tile) from stage st; `first`: no earlier
+    // unit of this segment, so there is no row tile 3 awaiting its fold.
+    int i = 0;
+    auto unit = [&](bool first) __attribute__((always_inline)) {
+        const int st = i & (NS - 1);
+        TileRef x = cur;
+        TileRef xprev = cur;
+        if (GSUM) xprev.g = first ? -1 : cur.g - 1;   // -1: nothing to store
+        // row tile 0, with the unpack of this unit's weights and the fold of the
+        // previous unit's last tile
+        read_a(a_nxt, 1);
+        float sbz = *reinterpret_cast<const float*>(lds + rsb);
+        sbz = lh ? 0.f : sbz;
+        // (for the first unit of a segment accB is zero: the fold adds exact zeros)
+        step(a_cur, accA, accB, facc[3], 3, xprev, true, true);
+        S = scales(sa_of(0), sbz);
+        // row tile 1, fold of tile 0
+        read_a(a_cur, 2);
+        step(a_nxt, accB, accA, facc[0], 0, x, false, true);
+        S = scales(sa_of(1), sbz);
+        // row tile 2, fold of tile 1
+        read_a(a_nxt, 3);
+        step(a_cur, accA, accB, facc[1], 1, x, false, true);
+        S = scales(sa_of(2), sbz);
+        const float sa3 = sa_of(3);   // read before the barrier: the stage is refilled after it
+        // row tile 3.  The DMA of unit i+1 has landed once at most the two younger
+        // units' loads are pending (three units in flight), and every wave has issued
+        // its last read of this stage (the barrier waits for LDS reads).  Near the
+        // end of the share fewer units are in flight; the first unit of a segment
+        // follows a flush, whose C stores are younger than that DMA and whose number
+        // depends on how many rows and columns of the tile exist; the group-sum
+        // variant stores as it goes.  In those cases no count bound is safe: drain.
+        if (GSUM || first || i + 3 >= n) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
+        __syncthreads();
+        if (i + 4 < n) {
+            advance_dma();
+            issue(st);
+        }
+        next_stage((st + 1) & (NS - 1));
+        read_b();
+        read_a(a_cur, 0);
+        step(a_nxt, accB, accA, facc[2], 2, x, false, true);
+        S = scales(sa3, sbz);
+        ++i;
+        if (GSUM) ++cur.g;
+    };
+    // segments: the units of one tile within this workgroup's share
+    while (i < n) {
+        const int g0 = (int)((u0 + i) % NG);
+        const int len = min(NG - g0, n - i);
+        if (GSUM) cur.g = g0;
+        accB = zero16;
+        S = zero16f;
+        for (int k = 0; k < len; k++) unit(k == 0);
+        // the segment's last row tile 3, then publish the segment
+        TileRef xl = cur;
+        if (GSUM) xl.g = cur.g - 1;
+#pragma unroll
+        for (int q = 0; q < 4; q++) fold_q(facc[3], accB, S, 3, q, xl);
+        flush(cur);
+        // the next unit's fragments, read again from its stage (still intact): the
+        // copies read during the last unit are then dead across the flush, which
+        // leaves the flush the registers it needs
+        read_b();
+        read_a(a_cur, 0);
+        // next tile
+        ++cur.t;
+        cur.bm += BM;
+        if (cur.bm >= ntm * BM) {
+            cur.bm = 0;
+            cur.bn += BN;
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 }  // namespace
 

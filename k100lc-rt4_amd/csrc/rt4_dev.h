@@ -11,6 +11,8 @@ constexpr int kWave = 64;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 // fp16 bit pattern -> fp32 (exact).
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
