@@ -22,12 +22,16 @@
 //     facc += f32(acc) * S,   S = sa * sb,   acc = 16*I exactly (x16 nibble unpack),
 // and the result is scaled by 1/16 once at the end (a power of two, so the bits
 // equal those of scaling every term).  S is formed on the matrix core: one
-// v_mfma_f32_32x32x1_2b_f32 per pair of row tiles gives the rank-1 products
-// sa (x) sb in the accumulator layout, each a single fp32 product rounded once.
+// v_mfma_f32_32x32x2_f32 per row tile (its k = 1 half zero) gives the rank-1
+// products sa (x) sb in the accumulator layout, each a single fp32 product
+// rounded once.  (The two-block form, one MFMA per pair of row tiles, needs 16
+// more registers live, which this loop does not have.)
 //
-// What bounds this kernel on gfx950 is instruction issue: a SIMD issues about one
-// instruction per 4 cycles whatever its kind (scalar, vector, LDS, MFMA issue),
-// and the fold alone is two vector instructions per output per group.  So the
+// What bounds this kernel on gfx950 is instruction issue: measured, a SIMD with
+// two such waves issues about one instruction per 4 cycles whatever its kind
+// (scalar, vector, LDS; an int8 MFMA takes about 16), with little overlap
+// between the two waves, and the fold alone is two vector instructions per
+// output per group (128 per wave per unit against 16 MFMAs).  So the
 // loop is built for few instructions: it is unrolled over the four LDS stages so
 // that every LDS address is a per-lane register plus an immediate offset; the DMA
 // sources are per-lane offsets (fixed while the tile is unchanged) plus scalar
