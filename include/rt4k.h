@@ -114,6 +114,19 @@ int rt4_gemv_w4a8_groupsums(int32_t* gsum, float* y, const uint32_t* wq, const u
 int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows,
                   int N, int K, void* stream);
 
+/* No counterpart in the reference: rt4_gemv_w4a8 for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, the same two launches and
+ * the same split, so y is bit-identical to rt4_gemv_w4a8's; it calls no
+ * hipMalloc, hipFree or other allocating routine.  Its scratch is one static
+ * device array per GPU (about 0.4 MB, held until the process ends): K <= 65536
+ * and at most 320 CUs, else RT4_E_SHAPE / RT4_E_ARG.  Every call on a GPU shares
+ * that GPU's array, so calls that overlap on one GPU (other streams, other host
+ * threads) race; order them.  The first call on a device clears the array's
+ * counters with a kernel on `stream`. */
+int rt4_gemv_w4a8_noalloc(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N,
+                          int K, void* stream);
+
 /* rt4_gemv_w4a8 as ONE launch, with an explicit launch configuration
  * (parameters as rt4_gemv_w4a8_q_cfg; tuning and tests): the GEMV's waves
  * quantize the activations in registers, codes and scales bit-identical to

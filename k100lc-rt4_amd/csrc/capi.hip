@@ -63,7 +63,7 @@ bool capturing(hipStream_t st) {
 // `zero`).  Growth under stream capture is refused with RT4_E_CAPTURE: one
 // eager call at the largest shape first sizes the scratch, after which capture
 // allocates nothing.
-int scratch(Slot slot, size_t bytes, void** out, hipStream_t st, bool zero = false) {
+int lib_scratch(Slot slot, size_t bytes, void** out, hipStream_t st, bool zero = false) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
@@ -146,8 +146,8 @@ int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const
     if (rc) return rc;
     const rt4::GemmPlan plan = rt4::gemm_plan(M, N, K, cus);
     void *part = nullptr, *cnt = nullptr;
-    if ((rc = scratch(kSlotGemmPart, plan.part_bytes, &part, st))) return rc;
-    if ((rc = scratch(kSlotGemmCnt, plan.cnt_bytes, &cnt, st, true))) return rc;
+    if ((rc = lib_scratch(kSlotGemmPart, plan.part_bytes, &part, st))) return rc;
+    if ((rc = lib_scratch(kSlotGemmCnt, plan.cnt_bytes, &cnt, st, true))) return rc;
     return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, plan, static_cast<float*>(part),
                                             static_cast<int*>(cnt), st),
                       who);
@@ -173,8 +173,8 @@ int gemv_split_ws(rt4::GemvSplit* sp, int cus, hipStream_t st) {
         return RT4_OK;
     }
     void *part = nullptr, *cnt = nullptr;
-    int rc = scratch(kSlotGemvPart, pb, &part, st);
-    if (rc || (rc = scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
+    int rc = lib_scratch(kSlotGemvPart, pb, &part, st);
+    if (rc || (rc = lib_scratch(kSlotGemvCnt, cb, &cnt, st, true))) return rc;
     sp->part = static_cast<float*>(part);
     sp->cnt = static_cast<int*>(cnt);
     return RT4_OK;
@@ -264,6 +264,22 @@ int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int w
     return RT4_OK;
 }
 
+// ---- The no-allocation decode linear (rt4_gemv_w4a8_noalloc).  Its scratch
+// is one file-scope device array, held by every device the library runs on until
+// the process ends: the quantized activations (4 rows of at most kNaMaxK codes
+// and their scales), then the split GEMV's partials and counters (sized, like the
+// allocated workspace, for one piece per CU, at most kNaMaxCus CUs).  In host code
+// `scratch` is not a device address: every use goes through the per-device
+// pointer that hipGetSymbolAddress returns.
+constexpr int kNaMaxK = 65536;
+constexpr int kNaMaxCus = 320;
+constexpr size_t kNaQ = (size_t)4 * kNaMaxK;                                       // int8 codes
+constexpr size_t kNaS = (size_t)4 * (kNaMaxK / 128) * sizeof(float);             // their scales
+constexpr size_t kNaP = (size_t)kNaMaxCus * rt4::kGemvMaxRb * 4 * 16 * sizeof(float);  // split partials
+constexpr size_t kNaC = (size_t)kNaMaxCus * sizeof(int);                          // split counters
+constexpr size_t kNaBytes = kNaQ + kNaS + kNaP + kNaC;
+static_assert(kNaQ % 256 == 0 && kNaS % 256 == 0 && kNaP % 256 == 0, "sections stay 256-byte aligned");
+
 int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
                    const int8_t* xq, const float* sc, int M, int N, int K, void* stream) {
     if (!c || !wq || !wsc_gm || !xq || !sc) return fail(RT4_E_ARG, "%s: null pointer", who);
@@ -274,6 +290,34 @@ int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq,
     return run_gemm(who, gsum, c, wq, wsc_gm, xq, sc, M, N, K, as_stream(stream));
 }
 
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNaBytes];
+
+namespace {
+std::mutex g_na_mu;
+unsigned char* g_na_ptr[kMaxDev] = {};
+
+// This device's address of `scratch`, looked up (and its split counters cleared
+// with a fill kernel on `st`) on the first call on the device.
+int noalloc_scratch(unsigned char** out, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDev) return fail(RT4_E_ARG, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (!g_na_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+        e = rt4::launch_zero_i32(reinterpret_cast<int*>(static_cast<unsigned char*>(ptr) + kNaQ + kNaS + kNaP),
+                                 kNaC / sizeof(int), st);
+        if (e != hipSuccess) return hip_status(e, "clearing the split counters");
+        g_na_ptr[dev] = static_cast<unsigned char*>(ptr);
+    }
+    *out = g_na_ptr[dev];
+    return RT4_OK;
+}
 }  // namespace
 
 namespace rt4 {
@@ -368,12 +412,45 @@ int rt4_gemv_w4a8(float* y, const uint32_t* wq, const uint16_t* ws, const float*
     // re-quantizes the activations in every tile and measures slower.)
     hipStream_t st = as_stream(stream);
     void *q = nullptr, *s = nullptr;
-    if ((rc = scratch(kSlotActQ, (size_t)rows * K, &q, st))) return rc;
-    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s, st))) return rc;
+    if ((rc = lib_scratch(kSlotActQ, (size_t)rows * K, &q, st))) return rc;
+    if ((rc = lib_scratch(kSlotActS, (size_t)rows * (K / 128) * sizeof(float), &s, st))) return rc;
     hipError_t e = rt4::launch_quant_act_a8(static_cast<int8_t*>(q), static_cast<float*>(s), nullptr, x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a8 quant launch");
     return run_gemv("k_gemv_w4a8 launch", nullptr, y, wq, ws, static_cast<const int8_t*>(q),
                     static_cast<const float*>(s), nullptr, rows, N, K, c, st);
+}
+
+int rt4_gemv_w4a8_noalloc(float* y, const uint32_t* wq, const uint16_t* ws, const float* x, int rows, int N,
+                          int K, void* stream) {
+    if (!y || !wq || !ws || !x) return fail(RT4_E_ARG, "rt4_gemv_w4a8_noalloc: null pointer");
+    int rc = check_gemv_shape("rt4_gemv_w4a8_noalloc", rows, N, K);
+    if (rc) return rc;
+    if (K > kNaMaxK)
+        return fail(RT4_E_SHAPE, "rt4_gemv_w4a8_noalloc: K=%d exceeds the static scratch (K <= %d)", K, kNaMaxK);
+    if (!aligned(wq, 16) || !aligned(y, 4) || !aligned(x, 4) || !aligned(ws, 4))
+        return fail(RT4_E_ARG, "rt4_gemv_w4a8_noalloc: misaligned pointer (wq needs 16 bytes, ws 4)");
+    int cus = 0;
+    if ((rc = device_cus(&cus))) return rc;
+    if (cus > kNaMaxCus)
+        return fail(RT4_E_ARG, "rt4_gemv_w4a8_noalloc: %d CUs exceed the static scratch (at most %d)", cus,
+                    kNaMaxCus);
+    rt4::GemvCfg c;
+    if ((rc = default_cfg(rows, N, K, &c))) return rc;
+    hipStream_t st = as_stream(stream);
+    unsigned char* p = nullptr;
+    if ((rc = noalloc_scratch(&p, st))) return rc;
+    int8_t* q = reinterpret_cast<int8_t*>(p);
+    float* s = reinterpret_cast<float*>(p + kNaQ);
+    // the same two launches and the same split as rt4_gemv_w4a8, so y is bit-identical
+    hipError_t e = rt4::launch_quant_act_a8(q, s, nullptr, x, rows, K, st);
+    if (e != hipSuccess) return hip_status(e, "rt4_gemv_w4a8_noalloc quant launch");
+    rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
+    if (sp.nrem > 0) {
+        sp.part = reinterpret_cast<float*>(p + kNaQ + kNaS);
+        sp.cnt = reinterpret_cast<int*>(p + kNaQ + kNaS + kNaP);
+    }
+    return hip_status(rt4::launch_gemv_w4a8(y, nullptr, wq, ws, q, s, nullptr, rows, N, K, c, sp, st),
+                      "rt4_gemv_w4a8_noalloc launch");
 }
 
 int rt4_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, const float* x,
@@ -456,8 +533,8 @@ int rt4_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, const float*
         return fail(RT4_E_ARG, "k_gemv_w4a4: misaligned pointer (wq needs 16 bytes, ws 4)");
     hipStream_t st = as_stream(stream);
     void *q = nullptr, *s = nullptr;
-    if ((rc = scratch(kSlotActQ, (size_t)rows * K / 2, &q, st))) return rc;
-    if ((rc = scratch(kSlotActS, (size_t)rows * (K / 32) * sizeof(float), &s, st))) return rc;
+    if ((rc = lib_scratch(kSlotActQ, (size_t)rows * K / 2, &q, st))) return rc;
+    if ((rc = lib_scratch(kSlotActS, (size_t)rows * (K / 32) * sizeof(float), &s, st))) return rc;
     hipError_t e = rt4::launch_quant_act_a4(static_cast<uint32_t*>(q), static_cast<float*>(s), x, rows, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemv_w4a4 quant launch");
     rt4::GemvCfg c;
@@ -482,7 +559,7 @@ int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint3
     // buffer for them).
     hipStream_t st = as_stream(stream);
     void* q = nullptr;
-    if ((rc = scratch(kSlotGemmA, (size_t)M * K, &q, st))) return rc;
+    if ((rc = lib_scratch(kSlotGemmA, (size_t)M * K, &q, st))) return rc;
     hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), nullptr, aq, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4 code expansion");
     return run_gemm("k_gemm_i4 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), asc_gm, M, N, K, st);
@@ -518,7 +595,7 @@ int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, 
     const size_t need = (size_t)M * K;
     hipStream_t st = as_stream(stream);
     void* q = c2;
-    if ((size_t)M * N * sizeof(float) < need && (rc = scratch(kSlotGemmA, need, &q, st))) return rc;
+    if ((size_t)M * N * sizeof(float) < need && (rc = lib_scratch(kSlotGemmA, need, &q, st))) return rc;
     hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4_a8 digit recombination");
     return run_gemm("k_gemm_i4_a8 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), sc, M, N, K, st);
@@ -589,7 +666,7 @@ int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, 
         !scratch_has(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit)))
         nsplit = 1;
     void* part = nullptr;
-    if (nsplit > 1 && (rc = scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st))) return rc;
+    if (nsplit > 1 && (rc = lib_scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st))) return rc;
     return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
                                           kv_cap, nsplit, static_cast<float*>(part), st),
                       "k_attention launch");

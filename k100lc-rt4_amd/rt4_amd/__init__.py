@@ -30,7 +30,7 @@ C_EXPORTS = (
     "rt4_last_error", "rt4_abi_version",
     "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
     "rt4_gemv_w4a8_groupsums",
-    "rt4_gemv_w4a8", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
+    "rt4_gemv_w4a8", "rt4_gemv_w4a8_noalloc", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
     "rt4_make_group_major", "rt4_quant_rows_a4", "rt4_quant_act_a4", "rt4_gemv_w4a4_q", "rt4_gemv_w4a4_q_cfg", "rt4_gemv_w4a4",
     "rt4_gemm_w4a4",
     "rt4_gemm_w4a8", "rt4_gemm_w4a8_i8", "rt4_gemm_w4a8_groupsums",
@@ -73,6 +73,7 @@ _SIGS = {
     "rt4_gemv_launch_plan": [_I, _I, _I, _P, _P, _P, _P],
     "rt4_gemv_w4a8_groupsums": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8": [_P, _P, _P, _P, _I, _I, _I, _P],
+    "rt4_gemv_w4a8_noalloc": [_P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a8_cfg": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_a8": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P],
     "rt4_quant_rows_i8": [_P, _P, _P, _I, _I, _I, _I, _P],

@@ -145,3 +145,13 @@ def test_gemm_rejects_shapes_beyond_32bit_offsets(rt4, M, N, K):
     assert L.rt4_gemm_w4a8_groupsums(W16, W16, W16, W16, W16, W16, M, N, K, None) == 1
     # the largest operands inside the range still pass the shape check (fail later on alignment)
     assert L.rt4_gemm_w4a8_i8(W16, ctypes.c_void_p(0x1004), W16, W16, W16, 838860, 64, 5120, None) == 2
+
+
+def test_noalloc_gemv_rejects_beyond_its_static_scratch(rt4):
+    """rt4_gemv_w4a8_noalloc has a fixed scratch (K <= 65536); larger K is an error, not an allocation."""
+    L = rt4.lib()
+    W16 = ctypes.c_void_p(0x1000)
+    assert L.rt4_gemv_w4a8_noalloc(W16, W16, W16, W16, 4, 64, 65536 + 128, None) == 1
+    assert "static scratch" in L.rt4_last_error().decode()
+    assert L.rt4_gemv_w4a8_noalloc(W16, W16, W16, W16, 5, 64, 256, None) == 1
+    assert L.rt4_gemv_w4a8_noalloc(W16, W16, ctypes.c_void_p(0x1002), W16, 4, 64, 256, None) == 2
