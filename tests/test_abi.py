@@ -112,6 +112,15 @@ def test_shim_attention_decode_branch_uses_callers_decode_kernel():
     assert "decode n_kv=300 kv_cap=4096 n_heads=24 ratio=6 n_q=64 max_split=8" in r.stdout
 
 
+def test_dropin_caller_is_built_and_links():
+    """tests/_bin/dropin_caller (built by __graft_entry__.build()) resolves librt4k.so
+    and the HIP runtime; with no arguments it prints its usage before any device work."""
+    exe = ROOT / "tests" / "_bin" / "dropin_caller"
+    assert exe.exists(), "built by __graft_entry__.build() (make -C tests dropin)"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stdout, (r.returncode, r.stdout, r.stderr)
+
+
 def test_single_hip_runtime_in_process(rt4):
     """librt4k.so binds to the HIP runtime torch already loaded (one runtime per process)."""
     import torch  # noqa: F401
