@@ -69,7 +69,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-kernel table beyond the roofline")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only launch the dominant kernels and a calibration copy, eagerly (for rocprofv3 --pmc)")
+                    help="only launch the dominant kernels (gate/up GEMV, gate/up GEMM, C4 attention) and a "
+                         "calibration copy, eagerly (for rocprofv3 --pmc)")
     return ap.parse_args()
 
 
@@ -107,11 +108,28 @@ def cpu_info() -> dict:
                 break
     except OSError:
         pass
-    return {"cpu": model, "os_cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+    lscpu = None
+    try:
+        import subprocess
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for line in r.stdout.splitlines():
+            if line.startswith("Model name:"):
+                lscpu = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"cpu": model, "lscpu_model": lscpu, "os_cpu_count": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
 
 
 def cpu_baseline(step_bytes: int, seconds: float) -> dict:
-    """The reference's CPU path for one decode MLP step, parallel over output rows."""
+    """The reference's CPU path (tools/rt4_io.py:40-52 dequant, then a float matmul,
+    tools/ref_full.py:113-117) on the GPU box's host cores, output rows split over
+    the cores with one BLAS thread each.  The decode MLP step is the reported value
+    (dequant + matmul per call, as the tools do); `extra` adds the same step with
+    the weights dequantised beforehand (matmul only), a row block of the C2 prefill
+    GEMM and a row block of the C3 LM head, each the median of at least 5 timed
+    repetitions after one warm-up."""
     import concurrent.futures as cf
 
     import numpy as np
@@ -120,42 +138,83 @@ def cpu_baseline(step_bytes: int, seconds: float) -> dict:
     from oracle import np_ref
 
     rng = np.random.default_rng(0)
-    M = 4
-    shapes = [(17408, 5120), (17408, 5120), (5120, 17408)]
-    mats = []
-    for N, K in shapes:
-        wq = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint32).view(np.uint8).reshape(N, K // 2)
-        ws = (np.abs(rng.standard_normal((N, K // 128))) * 0.01 + 1e-3).astype(np.float16).view(np.uint16)
-        x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
-        mats.append((wq, ws, np_ref.fake_quant_act(x)))
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
 
-    def linear(pool, wq, ws, xf):
-        N = wq.shape[0]
-        bounds = np.linspace(0, N, threads + 1).astype(int)
-        futs = [pool.submit(np_ref.cpu_linear, wq[a:b], ws[a:b], xf) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
-        return np.concatenate([f.result() for f in futs], axis=1)
+    def mat(N, K):
+        wq = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint32).view(np.uint8).reshape(N, K // 2)
+        ws = (np.abs(rng.standard_normal((N, K // 128))) * 0.01 + 1e-3).astype(np.float16).view(np.uint16)
+        return wq, ws
 
-    times = []
-    t_start = time.perf_counter()
-    with threadpoolctl.threadpool_limits(1), cf.ThreadPoolExecutor(threads) as pool:
-        while True:
+    def acts(M, K):
+        x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+        return np_ref.fake_quant_act(x)
+
+    def split(pool, fn, N, *args):
+        bounds = np.linspace(0, N, threads + 1).astype(int)
+        futs = [pool.submit(fn, a, b, *args) for a, b in zip(bounds[:-1], bounds[1:]) if b > a]
+        return [f.result() for f in futs]
+
+    def dq_mm(a, b, wq, ws, xf):           # (i) dequant + matmul of output rows [a, b)
+        return np_ref.cpu_linear(wq[a:b], ws[a:b], xf)
+
+    def mm(a, b, w, xf):                    # (ii) matmul only
+        return xf @ w[a:b].T
+
+    def timed(fn, min_reps=5, budget=seconds):
+        fn()                                # warm-up
+        ts, t_start = [], time.perf_counter()
+        while len(ts) < min_reps or (time.perf_counter() - t_start < budget and len(ts) < 20):
             t0 = time.perf_counter()
-            for wq, ws, xf in mats:
-                linear(pool, wq, ws, xf)
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_start > seconds or len(times) >= 20:
-                break
-    med = statistics.median(times)
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), len(ts)
+
+    M = 4
+    shapes = [(17408, 5120), (17408, 5120), (5120, 17408)]
+    mats = [mat(N, K) for N, K in shapes]
+    xs = [acts(M, K) for _, K in shapes]
+    out = {}
+    with threadpoolctl.threadpool_limits(1), cf.ThreadPoolExecutor(threads) as pool:
+        t_step, n_step = timed(lambda: [split(pool, dq_mm, wq.shape[0], wq, ws, xf)
+                                        for (wq, ws), xf in zip(mats, xs)], budget=seconds)
+        ws32 = [np_ref.dequant(wq, ws) for wq, ws in mats]
+        t_mm, n_mm = timed(lambda: [split(pool, mm, w.shape[0], w, xf) for w, xf in zip(ws32, xs)], budget=2.0)
+        out["decode_step_matmul_only"] = {"value": round(step_bytes / t_mm / 1e9, 3), "unit": "GB/s",
+                                          "ms_per_step": round(t_mm * 1e3, 2), "reps": n_mm,
+                                          "sample": "the same step, weights dequantised to fp32 beforehand"}
+        del ws32
+        # C2 prefill GEMM: M=1024 tokens, a block of 2048 of the 17408 gate/up rows
+        Mp, Nb, Kp = 1024, 2048, 5120
+        wq, ws = mat(Nb, Kp)
+        xp = rng.standard_normal((Mp, Kp)).astype(np.float32)
+        t_g, n_g = timed(lambda: split(pool, dq_mm, Nb, wq, ws, xp), budget=2.0)
+        w32 = np_ref.dequant(wq, ws)
+        t_gm, n_gm = timed(lambda: split(pool, mm, Nb, w32, xp), budget=2.0)
+        ops = 2.0 * Mp * Nb * Kp
+        out["prefill_gemm_c2_block"] = {
+            "TOPS": round(ops / t_g / 1e12, 4), "TOPS_matmul_only": round(ops / t_gm / 1e12, 4),
+            "us": round(t_g * 1e6, 1), "us_matmul_only": round(t_gm * 1e6, 1),
+            "us_full_N_extrapolated": round(t_g * 1e6 * 17408 / Nb, 1), "reps": [n_g, n_gm],
+            "sample": f"M={Mp}, K={Kp}, rows 0..{Nb} of N=17408 (dequant + matmul; and matmul only)"}
+        del w32, xp
+        # C3 LM head: M=4, K=5120, a block of 32768 of the 248320 rows, chunked by 8192
+        Nl = 32768
+        wq, ws = mat(Nl, 5120)
+        xf = acts(M, 5120)
+        t_l, n_l = timed(lambda: split(pool, dq_mm, Nl, wq, ws, xf), budget=2.0)
+        lb = Nl * 5120 // 2 + Nl * 40 * 2 + M * 5120 * 4 + M * Nl * 4
+        out["lm_head_c3_block"] = {"value": round(lb / t_l / 1e9, 3), "unit": "GB/s", "us": round(t_l * 1e6, 1),
+                                   "us_full_N_extrapolated": round(t_l * 1e6 * 248320 / Nl, 1), "reps": n_l,
+                                   "sample": f"M=4, K=5120, rows 0..{Nl} of N=248320 (dequant + matmul)"}
     try:
         blas = np.show_config(mode="dicts")["Build Dependencies"]["blas"]["name"]
     except Exception:  # noqa: BLE001
         blas = "unknown"
-    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "ms_per_step": round(med * 1e3, 2),
-            "sample": f"{len(times)} decode MLP steps (gate+up+down, M=4, 27B shapes), numpy RT4 dequant + "
+    return {"value": round(step_bytes / t_step / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(t_step * 1e3, 2),
+            "sample": f"{n_step} decode MLP steps (gate+up+down, M=4, 27B shapes), numpy RT4 dequant + "
                       f"matmul split over {threads} threads (1 BLAS thread each), median step",
-            "blas": blas, **cpu_info()}
+            "blas": blas, **cpu_info(), "extra": out}
 
 
 def gemm_table(torch, rt4_amd, workload, gen) -> dict:
@@ -287,7 +346,8 @@ def load_traffic(key: str):
 
 def pmc_probe(torch, rt4_amd, workload, gen) -> int:
     """Eager launches for counter collection: the gate/up GEMV over 16 distinct weight
-    sets (twice), the gate/up prefill GEMM 3 times, and 4 copies of COPY_BYTES."""
+    sets (twice), the gate/up prefill GEMM 3 times, the C4 attention prefill 3 times,
+    and 4 copies of COPY_BYTES."""
     import ctypes
 
     from rt4_amd import probe, profiling
@@ -308,6 +368,22 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
     c = torch.empty((Mg, Ng), device="cuda")
     for _ in range(3):
         rt4_amd.gemm_w4a8_i8(wq, sb, xq8, sc, out=c)
+    del wq, ws, sb, xg, xq8, sc, c
+    c4 = workload.ATTN_C4
+    n_q, ctx, H, KVH, D = c4["n_q"], c4["ctx"], c4["H"], c4["KVH"], c4["D"]
+    n_kv = ctx + n_q
+    q, k, v = workload.attn_torch(n_q, n_kv, H, KVH, D, generator=gen)
+    qq, qs = rt4_amd.attn_q_quant(q, n_q)
+    kc = torch.zeros((KVH, n_kv, D // 8), dtype=torch.int32, device="cuda")
+    ksc = torch.ones((KVH, 2, n_kv), device="cuda")
+    vc = torch.zeros((KVH, n_kv // 8, D), dtype=torch.int32, device="cuda")
+    vsc = torch.ones((KVH, n_kv // 64, D), device="cuda")
+    stage = torch.zeros((KVH, 64, D), device="cuda")
+    rt4_amd.kv_append_k(kc, ksc, k, 0)
+    rt4_amd.kv_append_v(vc, vsc, stage, v, 0)
+    for _ in range(3):
+        rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH)
+    del q, k, v, qq, qs, kc, ksc, vc, vsc, stage
     nb = profiling.COPY_BYTES
     src = torch.empty(nb // 4, dtype=torch.int32, device="cuda").random_()
     dst = torch.empty_like(src)
@@ -412,6 +488,9 @@ def main() -> int:
     g_, w_, rb_ = plan["groups_per_wave"], plan["waves"], plan["row_blocks"]
     # line-wise activation loads: one row block and their LDS slices within 64 KB (the launcher's rule)
     al = rb_ == 1 and w_ * 16 * g_ * 2 + w_ * M * 16 * 4 + w_ * M * g_ * 8 * 16 <= 65536
+    # measured ceiling: the fastest single launch that reads the same byte count
+    from rt4_amd import probe
+    ceil_gu = probe.read_ceiling(torch, gu_bytes, timed_graph=timed_graph)
     roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false> "
                           f"(gate/up GEMV, "
                           f"M={M} K={Kgu} N={Ngu}, "
@@ -419,7 +498,12 @@ def main() -> int:
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv_gate_up"),
                 "us_per_launch": round(gu_us, 3), "bytes_per_launch": gu_bytes,
-                "weight_only_GBs": round((Ngu * Kgu // 2) / (gu_us * 1e-6) / 1e9, 1)}
+                "weight_only_GBs": round((Ngu * Kgu // 2) / (gu_us * 1e-6) / 1e9, 1),
+                "measured_peak": {"value": ceil_gu["GBs"], "unit": "GB/s", "us": ceil_gu["us"],
+                                  "frac": round(achieved / ceil_gu["GBs"], 4),
+                                  "probe": f"one-pass read of the same {gu_bytes} bytes (rt4p_read_burst, "
+                                           f"{ceil_gu['blocks']}x{ceil_gu['threads']}, non-temporal), 16 buffers "
+                                           f"back to back in a graph"}}
 
     kernels = {}
     if not args.no_extra:
@@ -441,7 +525,11 @@ def main() -> int:
                 rt4_amd.gemv_w4a8_q(wq, ws, xq_d, sa_d, out=y_d)
 
         d_us = timed_graph(torch, gemv_d) * 1e3 / len(d_mats)
-        kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(gemv_kernel_bytes(M, Nd, Kd) / d_us / 1e3, 1)}
+        d_bytes = gemv_kernel_bytes(M, Nd, Kd)
+        ceil_d = probe.read_ceiling(torch, d_bytes, timed_graph=timed_graph)
+        kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(d_bytes / d_us / 1e3, 1),
+                                   "measured_peak_GBs": ceil_d["GBs"],
+                                   "frac_measured": round(d_bytes / d_us / 1e3 / ceil_d["GBs"], 4)}
 
         def gemv_gu_fused():   # its own best measured config: 4 groups per wave, 8 waves
             for wq, ws in gu_mats:
@@ -466,7 +554,14 @@ def main() -> int:
                 rt4_amd.gemv_w4a8_q(wq, ws, xq1, sa1, out=y1)
 
         c0_us = timed_graph(torch, gemv_c0) * 1e3 / len(c0_mats)
-        kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(gemv_kernel_bytes(1, 5120, 5120) / c0_us / 1e3, 1)}
+        c0_bytes = gemv_kernel_bytes(1, 5120, 5120)
+        ceil_c0 = probe.read_ceiling(torch, c0_bytes, timed_graph=timed_graph)
+        kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(c0_bytes / c0_us / 1e3, 1),
+                                 "measured_peak_GBs": ceil_c0["GBs"], "measured_peak_us": ceil_c0["us"],
+                                 "frac_measured": round(c0_bytes / c0_us / 1e3 / ceil_c0["GBs"], 4)}
+        kernels["ceilings"] = {"mfma_i32_16x16x64_i8_TOPS": probe.mfma_i8_rate(torch),
+                               "mfma_i32_32x32x32_i8_TOPS": probe.mfma_i8_rate(torch, big=True),
+                               "published_i8_TOPS": I8_PEAK_TOPS, "published_hbm_GBs": HBM_PEAK_GBS}
         # LM head (C3): M=4, K=5120, N=248320, two 0.66 GB copies alternated
         del layers, gu_mats, d_mats, c0_mats
         torch.cuda.empty_cache()

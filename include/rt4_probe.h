@@ -23,6 +23,12 @@ extern "C" {
 
 /* Stream `bytes` (multiple of 16) of `buf` through dwordx4 loads, `blocks` x 256 threads. */
 int rt4p_hbm_read(const void* buf, size_t bytes, void* sink, int blocks, void* stream);
+/* One pass over `bytes` (multiple of 16): `blocks` workgroups of `threads` (64..1024,
+ * a multiple of 64) each read one contiguous slice, every lane issuing all of its
+ * dwordx4 loads (at most 16; returns 1 if the slice needs more) before using any;
+ * nontemporal != 0 marks them non-temporal. */
+int rt4p_read_burst(const void* buf, size_t bytes, void* sink, int blocks, int threads, int nontemporal,
+                    void* stream);
 /* dst[0:bytes] = src[0:bytes] (bytes multiple of 16), `blocks` x 256 threads. */
 int rt4p_copy(void* dst, const void* src, size_t bytes, int blocks, void* stream);
 /* `iters` x 4 independent int8 MFMAs per wave: big != 0 selects

@@ -1,4 +1,4 @@
-"""HBM traffic per launch from rocprofv3 counter runs.
+"""HBM traffic and instruction mix per launch from rocprofv3 counter runs.
 
 `bench.py --pmc-probe` launches the dominant kernels of the benchmark eagerly
 next to a plain copy kernel (rt4p_copy) of known size.  Two counter runs of it,
@@ -10,6 +10,23 @@ give per-dispatch kilobyte counts.  `python -m rt4_amd.profiling <fetch.csv>
 <write.csv> <out.json>` scales each counter by what it reads for the copy
 (the copy moves exactly COPY_BYTES in and out), averages it per kernel and
 writes the bytes per launch that bench.py reports as roofline.traffic.
+
+Two further runs collect the shader counters of the same launches (at most 8
+SQ counters per run):
+
+    rocprofv3 --pmc SQ_WAVES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_VMEM SQ_INSTS_LDS SQ_INSTS_SALU \
+        SQ_INSTS_SMEM SQ_INSTS_BRANCH --output-format csv -d <dir> -o sqa -- python3 bench.py --pmc-probe
+    rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_ANY \
+        SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE --output-format csv -d <dir> -o sqb \
+        -- python3 bench.py --pmc-probe
+
+and `python -m rt4_amd.profiling sq <sqa.csv> <sqb.csv> <out.json>` writes the
+mean per dispatch of every counter for each kernel of KERNELS, with the derived
+fractions: MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES, summed over the SIMDs, per SIMD
+per cycle of the dispatch; GRBM_GUI_ACTIVE is summed over the XCDs, 32 CUs
+each, so cycles = GRBM_GUI_ACTIVE / XCDs), VALU-active and waiting shares of the
+wave cycles (SQ_ACTIVE_INST_VALU, SQ_WAIT_ANY over SQ_WAVE_CYCLES, all in
+quad-cycles) and instructions per wave.
 """
 from __future__ import annotations
 
@@ -23,7 +40,10 @@ COPY_KERNEL = "copy_k("          # the probe library's plain copy kernel
 KERNELS = {                       # report key -> substring of the rocprof kernel name
     "gemv_gate_up": "gemv_w4a8_k<4",
     "gemm_gate_up": "gemm_w4a8_k<false>",
+    "attention_c4": "fa_int4_k",
 }
+SIMDS_PER_CU = 4
+CUS_PER_XCD = 32
 
 
 def per_kernel(path: str, counter: str) -> dict[str, list[float]]:
@@ -69,7 +89,61 @@ def summarize(fetch_csv: str, write_csv: str) -> dict:
     return res
 
 
+def all_counters(path: str) -> dict[str, dict[str, list[float]]]:
+    """{counter: {kernel name: [value per dispatch]}} of a counter-collection CSV."""
+    out: dict[str, dict[str, list[float]]] = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            out.setdefault(row["Counter_Name"], {}).setdefault(row["Kernel_Name"], []).append(
+                float(row["Counter_Value"]))
+    return out
+
+
+def summarize_sq(paths: list[str], cus: int) -> dict:
+    res: dict = {"cus": cus}
+    tables = {}
+    for path in paths:
+        tables.update(all_counters(path))
+    for key, needle in KERNELS.items():
+        d: dict = {}
+        for counter, t in sorted(tables.items()):
+            v = pick(t, needle)
+            if v:
+                d[counter] = round(statistics.mean(v), 1)
+                d.setdefault("dispatches", len(v))
+        if not d:
+            continue
+        wc = d.get("SQ_WAVE_CYCLES")
+        if d.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None and d.get("GRBM_GUI_ACTIVE"):
+            cycles = d["GRBM_GUI_ACTIVE"] / max(1, cus // CUS_PER_XCD)
+            d["dispatch_cycles"] = round(cycles)
+            d["mfma_busy_frac"] = round(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * cus * SIMDS_PER_CU), 4)
+        if wc:
+            for c, name in (("SQ_ACTIVE_INST_VALU", "valu_active_frac"), ("SQ_WAIT_ANY", "wait_any_frac"),
+                            ("SQ_WAIT_INST_ANY", "wait_inst_frac"), ("SQ_ACTIVE_INST_ANY", "issue_any_frac")):
+                if d.get(c) is not None:
+                    d[name] = round(d[c] / wc, 4)
+        if d.get("SQ_WAVES"):
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VMEM", "SQ_INSTS_LDS", "SQ_INSTS_SALU"):
+                if d.get(c) is not None:
+                    d[c.replace("SQ_INSTS_", "per_wave_").lower()] = round(d[c] / d["SQ_WAVES"], 1)
+        res[key] = d
+    return res
+
+
 def main(argv: list[str]) -> int:
+    if len(argv) >= 2 and argv[1] == "sq":
+        if len(argv) != 5:
+            print(__doc__, file=sys.stderr)
+            return 2
+        import os
+        cus = int(os.environ.get("RT4_CUS", "256"))
+        res = summarize_sq(argv[2:4], cus)
+        with open(argv[4], "w") as f:
+            json.dump(res, f, indent=1)
+            f.write("\n")
+        print(json.dumps(res))
+        return 0
     if len(argv) != 4:
         print(__doc__, file=sys.stderr)
         return 2
