@@ -79,11 +79,15 @@ void k_attention_decode(float* out, const u32* qq, const float* qsc, const u32* 
                         const u32* vc, const float* vsc, int n_kv, int kv_cap, int n_heads, int ratio, int n_q,
                         float* pout, float* pmax, float* psum, int max_split) __attribute__((weak));
 
-// src/k_fa.hip:282-300
+// src/k_fa.hip:282-300.  RT_ATTN_OLD=1 sends the decode branch to the prefill
+// kernel, as the reference dispatcher does (src/k_fa.hip:287); RT_NSPLIT belongs
+// to the decode routine (src/k_fa.hip:251) and is read there, by the caller's
+// own k_attention_decode.
 void k_attention(float* out, const u32* qq, const float* qsc, const u32* kc, const float* ksc, const u32* vc,
                  const float* vsc, int n_q, int n_row, int n_kv, int off, int n_tile, int n_heads, int ratio,
                  int kv_cap, float* pout, float* pmax, float* psum, int max_split) {
-    if (n_row == 1 && off + 1 == n_kv && k_attention_decode) {
+    static const int old = getenv("RT_ATTN_OLD") ? atoi(getenv("RT_ATTN_OLD")) : 0;
+    if (n_row == 1 && off + 1 == n_kv && !old && k_attention_decode) {
         k_attention_decode(out, qq, qsc, kc, ksc, vc, vsc, n_kv, kv_cap, n_heads, ratio, n_q, pout, pmax, psum,
                            max_split);
         return;

@@ -112,6 +112,26 @@ def test_shim_attention_decode_branch_uses_callers_decode_kernel():
     assert "decode n_kv=300 kv_cap=4096 n_heads=24 ratio=6 n_q=64 max_split=8" in r.stdout
 
 
+def test_shim_attention_old_switch_takes_the_prefill_kernel():
+    """RT_ATTN_OLD=1 sends the decode branch to the prefill kernel, as the reference
+    dispatcher does (src/k_fa.hip:287), even when the executable defines its own
+    decode routine: the prefill entry's argument check (null pointers) then ends
+    the caller with the reference's exit(1), before any device work."""
+    import os
+    src = ROOT / "tests" / "shim_decode_caller.cpp"
+    exe = ROOT / "tests" / "_shim_decode_caller_old"
+    lib = ROOT / "k100lc-rt4_amd" / "rt4_amd" / "lib"
+    subprocess.run(["g++", "-std=c++17", "-I", str(ROOT / "include"), str(src), "-L", str(lib),
+                    "-lrt4k", f"-Wl,-rpath,{lib}", "-o", str(exe)], check=True)
+    try:
+        r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60,
+                           env={**os.environ, "RT_ATTN_OLD": "1"})
+    finally:
+        exe.unlink(missing_ok=True)
+    assert r.returncode == 1, (r.returncode, r.stdout, r.stderr)
+    assert "k_attention" in r.stdout and "decode n_kv" not in r.stdout
+
+
 def test_dropin_caller_is_built_and_links():
     """tests/_bin/dropin_caller (built by __graft_entry__.build()) resolves librt4k.so
     and the HIP runtime; with no arguments it prints its usage before any device work."""
