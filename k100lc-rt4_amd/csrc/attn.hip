@@ -34,8 +34,6 @@
 // issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.
-#include <type_traits>
-
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -51,6 +49,18 @@ constexpr int NTA = 256;          // 4 waves
 constexpr float L2E = 1.4426950408889634f;
 constexpr int KU_BYTES = 4 * 4 * 64 * 16;   // unpacked K operands of one tile
 constexpr int VU_BYTES = 16 * 64 * 16;      // unpacked V operands of one tile
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Products x[4G + r] * y for r = 0..3 in the 16x16 accumulator layout (lane l =
+// 16G + i holds rows 4G..4G+3 of column i), on the matrix core: v_mfma_f32_4x4x1
+// gives lane l, output r, the A operand of lane 4(l/4) + r times the B operand of
+// lane l, so A = x[4G + (l & 3)] and B = the lane's own y.  Each output is the one
+// fp32 rounding of the product, as a v_mul_f32 would give.
+__device__ __forceinline__ v4f outer4(float x_of_lane, float y) {
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    return __builtin_amdgcn_mfma_f32_4x4x1f32(x_of_lane, y, z, 0, 0, 0);
+}
 
 __device__ __forceinline__ int sext4(uint32_t w, int e) { return ((int)(w << (28 - 4 * e))) >> 28; }
 
@@ -321,45 +331,48 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // buffers hold unpacked operands (one read by the tile being computed, one
     // written with the next tile), so each tile costs one barrier.
     struct Stage {
-        uint4 k0, k1;                   // key tid%64, dwords 8p..8p+7 (p = tid/64)
+        v4u k0, k1;                     // key tid%64, dwords 8p..8p+7 (p = tid/64)
         uint32_t v[8];                  // dim tid, 8-key groups 0..7
         float ks, vs;
     };
-    // Branch-free loads with addresses clamped into the cache; the out-of-range
-    // values are replaced (zero codes, unit scales) only when the stage is
-    // unpacked.  Selecting right after a load, or loading under a condition, makes
-    // the compiler wait for the load there, which would defeat the prefetch.
+    // Buffer loads: a per-lane offset fixed for the whole loop plus a per-tile
+    // scalar offset, and the buffer's range check supplies the reference's zero
+    // codes -- the K resource ends at key n_kv, the V resource at the last whole
+    // 8-key group (flash_attn_core.h:143-152), so reads past them return 0 with no
+    // memory access.  Scales past kv_cap are replaced by 1 when the stage is
+    // unpacked.  No load is conditional or clamped: selecting right after a load,
+    // or loading under a condition, makes the compiler wait for the load there,
+    // which would defeat the prefetch.
+    constexpr int kRsrcW3 = 0x00020000;    // dword 3 of the resource: 32-bit data format
+    const __amdgpu_buffer_rsrc_t rs_k =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(kc), 0, n_kv * KDW * 4, kRsrcW3);
+    const __amdgpu_buffer_rsrc_t rs_v =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(vc), 0, (n_kv / 8) * HD * 4, kRsrcW3);
+    const __amdgpu_buffer_rsrc_t rs_ks =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(ksc), 0, 2 * kv_cap * 4, kRsrcW3);
+    const __amdgpu_buffer_rsrc_t rs_vs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vsc), 0, (kv_cap / BNK) * HD * 4, kRsrcW3);
+    const int off_k = ((tid & 63) * KDW + 8 * (tid >> 6)) * 4;          // + tile * BNK * KDW * 4
+    const int off_ks = (((tid >> 6) & 1) * kv_cap + (tid & 63)) * 4;    // + tile * BNK * 4
     auto load = [&](Stage& S, int t) {
-        const int kb = t * BNK;
-        const int kk = tid & 63, p = tid >> 6;
-        const int krow = kb + kk < n_kv ? kb + kk : 0;
-        const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)krow * KDW + 8 * p);
-        S.k0 = src[0];
-        S.k1 = src[1];
+        const int sk = t * (BNK * KDW * 4), sv = t * (BNK / 8 * HD * 4);
+        S.k0 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k, sk, 0);
+        S.k1 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k + 16, sk, 0);
 #pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const int k8 = kb / 8 + g;
-            S.v[g] = vc[(size_t)(k8 * 8 + 8 <= n_kv ? k8 : 0) * HD + tid];
-        }
-        const int j = kb + (tid & 63);
-        S.ks = ksc[(size_t)((tid >> 6) & 1) * kv_cap + (tid < 2 * BNK && j < kv_cap ? j : 0)];
-        S.vs = vsc[(size_t)(t < kv_cap / BNK ? t : 0) * HD + tid];
+        for (int g = 0; g < 8; g++)
+            S.v[g] = __builtin_amdgcn_raw_buffer_load_b32(rs_v, tid * 4 + (g & 3) * HD * 4,
+                                                          sv + (g >> 2) * 4 * HD * 4, 0);
+        S.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_ks, off_ks, t * BNK * 4, 0));
+        S.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_vs, tid * 4, t * HD * 4, 0));
     };
-    // WHOLE: the tile lies wholly below n_kv and needs none of the zero
-    // substitutions (the caller picks the instance with a uniform branch).
-    auto store = [&](const Stage& S, int b, int t, auto whole_tag) {
-        constexpr bool whole = decltype(whole_tag)::value;
+    auto store = [&](const Stage& S, int b, int t) {
         const int kb = t * BNK;
         unsigned char* kub = ku + b * KU_BYTES;
         unsigned char* vub = vu + b * VU_BYTES;
         {   // K: x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16;
             // keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
             const int kk = tid & 63, p = tid >> 6;
-            const bool kin = kb + kk < n_kv;
-            uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
-            if constexpr (!whole)
-#pragma unroll
-                for (int g = 0; g < 8; g++) d[g] = kin ? d[g] : 0u;
+            const uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
@@ -369,16 +382,11 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         }
         {   // V: lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3
             // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
-            uint32_t e[8], o[8], vv[8];
-#pragma unroll
-            for (int g = 0; g < 8; g++) vv[g] = S.v[g];
-            if constexpr (!whole)
-#pragma unroll
-                for (int g = 0; g < 8; g++) vv[g] = (kb / 8 + g) * 8 + 8 <= n_kv ? vv[g] : 0u;
+            uint32_t e[8], o[8];
 #pragma unroll
             for (int g = 0; g < 8; g++) {
-                e[g] = even_x16(vv[g]);
-                o[g] = odd_x16(vv[g]);
+                e[g] = even_x16(S.v[g]);
+                o[g] = odd_x16(S.v[g]);
             }
 #pragma unroll
             for (int g = 0; g < 4; g++) {
@@ -393,10 +401,6 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         }
         if (tid < 2 * BNK) ks_l[b][tid] = kb + (tid & 63) < kv_cap ? S.ks : 1.f;
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
-    };
-    auto store_tile = [&](const Stage& S, int b, int t) {
-        if ((t + 1) * BNK <= n_kv) store(S, b, t, std::true_type{});
-        else store(S, b, t, std::false_type{});
     };
 
     const v4i zero = {0, 0, 0, 0};
@@ -415,12 +419,11 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[64], qop[1], a0, 0, 0, 0);
             v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
             a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
-            const float4 k0 = *reinterpret_cast<const float4*>(ksb + 16 * kt + 4 * G);
-            const float4 k1 = *reinterpret_cast<const float4*>(ksb + BNK + 16 * kt + 4 * G);
-            const float s0[4] = {k0.x, k0.y, k0.z, k0.w}, s1[4] = {k1.x, k1.y, k1.z, k1.w};
+            // key scale x query scale of each entry, then S = a1 * c1 + a0 * c0
+            const v4f c0 = outer4(ksb[16 * kt + 4 * G + (lane & 3)], A0);
+            const v4f c1 = outer4(ksb[BNK + 16 * kt + 4 * G + (lane & 3)], A1);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                sv[kt][r] = fmaf((float)a1[r], s1[r] * A1, (float)a0[r] * (s0[r] * A0));
+            for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[r], (float)a0[r] * c0[r]);
         }
         if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
 #pragma unroll
@@ -435,8 +438,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) m = fmaxf(m, sv[kt][r]);
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        {   // xor 16 and xor 32 partners: each swap leaves a lane its value and its partner's
+            const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+            m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+            const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+            m = fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+        }
         // Fully masked row in this tile: take the running reference, so alpha = 1 and
         // every P is 2^(-inf) = 0.  (The reference masks with -1e30 and reaches this
         // only after a visible tile; -inf gives the same P there and also keeps a row
@@ -467,10 +474,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
         const int isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, pop, zero, 0, 0, 0)[0];
         const float r_new = fmaxf(rref, m);
-        const float alpha = exp2f(rref - r_new);
-        const float beta = exp2f(m - r_new);
+        // v_exp_f32 directly: both arguments are <= 0, and a factor below 2^-126
+        // (flushed to zero) scales contributions that no longer count
+        const float alpha = __builtin_amdgcn_exp2f(rref - r_new);
+        const float beta = __builtin_amdgcn_exp2f(m - r_new);
         const float pb = beta * (1.f / 7.f);
-        L = L * alpha + (float)isum * (beta / 7.f);
+        L = L * alpha + (float)isum * pb;
         rref = r_new;
         // ---- O^T = V^T P^T, folded per dim tile
         const float pb16 = pb * 0.0625f;          // V is x16 unpacked
@@ -486,17 +495,16 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         for (int dt = 0; dt < 16; dt++) {
             const v4i va = *(reinterpret_cast<const v4i*>(vub) + dt * 64 + lane);
             const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pop, zero, 0, 0, 0);
-            const float4 s4 = *reinterpret_cast<const float4*>(vsb + 16 * dt + 4 * G);
-            const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+            const v4f ps = outer4(vsb[16 * dt + 4 * G + (lane & 3)], pb16);   // vsc * pb16
 #pragma unroll
-            for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], pb16 * sc[r], O[dt][r]);
+            for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], ps[r], O[dt][r]);
         }
     };
 
     Stage S;
     if (t0 < t1) {
         load(S, t0);
-        store_tile(S, t0 & 1, t0);
+        store(S, t0 & 1, t0);
         if (t0 + 1 < t1) load(S, t0 + 1);
     }
     __syncthreads();
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // compute tile t.  Storing before computing keeps S's registers free during
         // the compute phase.
         if (t + 1 < t1) {
-            store_tile(S, (t + 1) & 1, t + 1);
+            store(S, (t + 1) & 1, t + 1);
             if (t + 2 < t1) load(S, t + 2);
         }
         // keep the loads here: left to itself the compiler sinks them next to their
