@@ -34,6 +34,8 @@
 // issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.
+#include <type_traits>
+
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -326,23 +328,34 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         for (int r = 0; r < 4; r++) O[dt][r] = 0.f;
     float rref = -1e30f, L = 0.f;
 
-    // Pipeline: one register set stages the packed K/V of the next tile (its
-    // global loads are in flight during a whole tile of compute) and two LDS
-    // buffers hold unpacked operands (one read by the tile being computed, one
-    // written with the next tile), so each tile costs one barrier.
-    struct Stage {
+    // Pipeline over the 64-key tiles.  P of a tile uses that tile's own max, so
+    // S, the mask, the tile max and P of tile t+1 do not depend on tile t: each
+    // iteration runs the O update and PV product of tile t ("back") beside S and P
+    // of tile t+1 ("front"), two independent chains for the scheduler.  K runs one
+    // tile ahead of V: during iteration t the LDS buffers hold K(t+1) (read by
+    // front) and V(t) (read by back) while the other K and V buffers take K(t+2)
+    // and V(t+1) from registers staged during the previous iteration, whose global
+    // loads (K(t+3), V(t+2)) are issued right after; one barrier per tile orders
+    // every write after the reads of the buffer's previous tile.  Loads and stores
+    // past the split's last tile are harmless (range-checked buffer loads, LDS
+    // slots nobody reads) and are left unguarded, so an iteration is one basic
+    // block apart from the O rescale, which comes first.
+    struct StageK {
         v4u k0, k1;                     // key tid%64, dwords 8p..8p+7 (p = tid/64)
+        float ks;
+    };
+    struct StageV {
         uint32_t v[8];                  // dim tid, 8-key groups 0..7
-        float ks, vs;
+        float vs;
     };
     // Buffer loads: a per-lane offset fixed for the whole loop plus a per-tile
-    // scalar offset, and the buffer's range check supplies the reference's zero
-    // codes -- the K resource ends at key n_kv, the V resource at the last whole
-    // 8-key group (flash_attn_core.h:143-152), so reads past them return 0 with no
-    // memory access.  Scales past kv_cap are replaced by 1 when the stage is
-    // unpacked.  No load is conditional or clamped: selecting right after a load,
-    // or loading under a condition, makes the compiler wait for the load there,
-    // which would defeat the prefetch.
+    // scalar offset, and the buffer's range check (which includes the scalar
+    // offset) supplies the reference's zero codes -- the K resource ends at key
+    // n_kv, the V resource at the last whole 8-key group (flash_attn_core.h:
+    // 143-152), so reads past them return 0 with no memory access.  Scales past
+    // kv_cap are replaced by 1 when the stage is unpacked.  No load is conditional
+    // or clamped: selecting right after a load, or loading under a condition,
+    // makes the compiler wait for the load there, which would defeat the prefetch.
     constexpr int kRsrcW3 = 0x00020000;    // dword 3 of the resource: 32-bit data format
     const __amdgpu_buffer_rsrc_t rs_k =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(kc), 0, n_kv * KDW * 4, kRsrcW3);
@@ -354,63 +367,71 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vsc), 0, (kv_cap / BNK) * HD * 4, kRsrcW3);
     const int off_k = ((tid & 63) * KDW + 8 * (tid >> 6)) * 4;          // + tile * BNK * KDW * 4
     const int off_ks = (((tid >> 6) & 1) * kv_cap + (tid & 63)) * 4;    // + tile * BNK * 4
-    auto load = [&](Stage& S, int t) {
-        const int sk = t * (BNK * KDW * 4), sv = t * (BNK / 8 * HD * 4);
+    auto load_k = [&](StageK& S, int t) {
+        const int sk = t * (BNK * KDW * 4);
         S.k0 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k, sk, 0);
         S.k1 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k + 16, sk, 0);
+        S.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_ks, off_ks, t * BNK * 4, 0));
+    };
+    auto load_v = [&](StageV& S, int t) {
+        const int sv = t * (BNK / 8 * HD * 4);
 #pragma unroll
         for (int g = 0; g < 8; g++)
             S.v[g] = __builtin_amdgcn_raw_buffer_load_b32(rs_v, tid * 4 + (g & 3) * HD * 4,
                                                           sv + (g >> 2) * 4 * HD * 4, 0);
-        S.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_ks, off_ks, t * BNK * 4, 0));
         S.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_vs, tid * 4, t * HD * 4, 0));
     };
-    auto store = [&](const Stage& S, int b, int t) {
-        const int kb = t * BNK;
+    auto store_k = [&](const StageK& S, int b, int t) {
+        // x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16;
+        // keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
         unsigned char* kub = ku + b * KU_BYTES;
+        const int kk = tid & 63, p = tid >> 6;
+        const uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
+                                       odd_x16(d[2 * g + 1]));
+            *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
+        }
+        if (tid < 2 * BNK) ks_l[b][tid] = t * BNK + (tid & 63) < kv_cap ? S.ks : 1.f;
+    };
+    auto store_v = [&](const StageV& S, int b, int t) {
+        // lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3;
+        // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
         unsigned char* vub = vu + b * VU_BYTES;
-        {   // K: x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16;
-            // keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
-            const int kk = tid & 63, p = tid >> 6;
-            const uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
+        uint32_t e[8], o[8];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
-                                           odd_x16(d[2 * g + 1]));
-                *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
-            }
+        for (int g = 0; g < 8; g++) {
+            e[g] = even_x16(S.v[g]);
+            o[g] = odd_x16(S.v[g]);
         }
-        {   // V: lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3
-            // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
-            uint32_t e[8], o[8];
 #pragma unroll
-            for (int g = 0; g < 8; g++) {
-                e[g] = even_x16(S.v[g]);
-                o[g] = odd_x16(S.v[g]);
-            }
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint32_t sel = (g & 1) ? 0x07060302u : 0x05040100u;
-                uint4 v;
-                v.x = __builtin_amdgcn_perm(o[0 + (g >> 1)], e[0 + (g >> 1)], sel);
-                v.y = __builtin_amdgcn_perm(o[2 + (g >> 1)], e[2 + (g >> 1)], sel);
-                v.z = __builtin_amdgcn_perm(o[4 + (g >> 1)], e[4 + (g >> 1)], sel);
-                v.w = __builtin_amdgcn_perm(o[6 + (g >> 1)], e[6 + (g >> 1)], sel);
-                *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
-            }
+        for (int g = 0; g < 4; g++) {
+            const uint32_t sel = (g & 1) ? 0x07060302u : 0x05040100u;
+            uint4 v;
+            v.x = __builtin_amdgcn_perm(o[0 + (g >> 1)], e[0 + (g >> 1)], sel);
+            v.y = __builtin_amdgcn_perm(o[2 + (g >> 1)], e[2 + (g >> 1)], sel);
+            v.z = __builtin_amdgcn_perm(o[4 + (g >> 1)], e[4 + (g >> 1)], sel);
+            v.w = __builtin_amdgcn_perm(o[6 + (g >> 1)], e[6 + (g >> 1)], sel);
+            *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
         }
-        if (tid < 2 * BNK) ks_l[b][tid] = kb + (tid & 63) < kv_cap ? S.ks : 1.f;
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
     };
 
     const v4i zero = {0, 0, 0, 0};
-    auto compute = [&](int t, int b) {
+    // front of tile t (K in buffer b): S^T = K Q^T for the 4 subtiles of 16 keys,
+    // the causal mask (MASK: the tile may reach past a row of this workgroup), the
+    // tile max m of each row, the P codes as the PV operand and their row sum.
+    struct Front {
+        v4i pop;
+        float m;
+        int isum;
+    };
+    auto front = [&](int t, int b, auto mask_tag) -> Front {
+        constexpr bool MASK = decltype(mask_tag)::value;
         const int kb = t * BNK;
         const unsigned char* kub = ku + b * KU_BYTES;
-        const unsigned char* vub = vu + b * VU_BYTES;
         const float* ksb = ks_l[b];
-        const float* vsb = vs_l[b];
-        // ---- S^T = K Q^T for the 4 subtiles of 16 keys
         float sv[4][4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
@@ -425,12 +446,14 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 #pragma unroll
             for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[r], (float)a0[r] * c0[r]);
         }
-        if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
+        if constexpr (MASK) {
+            if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+                for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -__builtin_inff();
+                    for (int r = 0; r < 4; r++)
+                        if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -__builtin_inff();
+            }
         }
         // ---- tile row max over the 64 keys of this lane's query
         float m = sv[0][0];
@@ -444,10 +467,11 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
             m = fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
         }
-        // Fully masked row in this tile: take the running reference, so alpha = 1 and
-        // every P is 2^(-inf) = 0.  (The reference masks with -1e30 and reaches this
-        // only after a visible tile; -inf gives the same P there and also keeps a row
-        // that has seen nothing yet -- possible at the start of a KV split -- at zero.)
+        // Fully masked row in this tile: take the running reference (the state after
+        // the previous tile), so alpha = 1 and every P is 2^(-inf) = 0.  (The
+        // reference masks with -1e30 and reaches this only after a visible tile;
+        // -inf gives the same P there and also keeps a row that has seen nothing
+        // yet -- possible at the start of a KV split -- at zero.)
         if (m < -1e29f) m = rref;
         // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand.
         // The clamp of the reference never binds here: m is the max of the row's S
@@ -468,21 +492,27 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             }
             pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[2] << 8 | (uint32_t)pq[1] << 16 | (uint32_t)pq[3] << 24;
         }
-        const v4i pop = {(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        Front f;
+        f.pop = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        f.m = m;
         // Σ_k P of the row over the tile's 64 keys on the matrix pipe: an A operand
         // of ones gives it in every output row (exact integers)
         const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-        const int isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, pop, zero, 0, 0, 0)[0];
-        const float r_new = fmaxf(rref, m);
+        f.isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, f.pop, zero, 0, 0, 0)[0];
+        return f;
+    };
+    // Online update with a tile's (m, row sum): the running reference, L, and O
+    // rescaled by alpha.  Returns the P scale beta/7 times the 1/16 of the x16 V
+    // operand.
+    auto update = [&](const Front& f) -> float {
+        const float r_new = fmaxf(rref, f.m);
         // v_exp_f32 directly: both arguments are <= 0, and a factor below 2^-126
         // (flushed to zero) scales contributions that no longer count
         const float alpha = __builtin_amdgcn_exp2f(rref - r_new);
-        const float beta = __builtin_amdgcn_exp2f(m - r_new);
+        const float beta = __builtin_amdgcn_exp2f(f.m - r_new);
         const float pb = beta * (1.f / 7.f);
-        L = L * alpha + (float)isum * pb;
+        L = L * alpha + (float)f.isum * pb;
         rref = r_new;
-        // ---- O^T = V^T P^T, folded per dim tile
-        const float pb16 = pb * 0.0625f;          // V is x16 unpacked
         // O * alpha is exact when alpha == 1 (running max unchanged): skip it when
         // that holds for every row of the wave (a wave-uniform branch)
         if (!__all(alpha == 1.f)) {
@@ -491,6 +521,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 #pragma unroll
                 for (int r = 0; r < 4; r++) O[dt][r] *= alpha;
         }
+        return pb * 0.0625f;
+    };
+    // back: O^T += (V^T P^T) * vsc * pb16 per dim tile, V in buffer b
+    auto back = [&](const v4i pop, float pb16, int b) {
+        const unsigned char* vub = vu + b * VU_BYTES;
+        const float* vsb = vs_l[b];
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) {
             const v4i va = *(reinterpret_cast<const v4i*>(vub) + dt * 64 + lane);
@@ -501,27 +537,41 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         }
     };
 
-    Stage S;
-    if (t0 < t1) {
-        load(S, t0);
-        store(S, t0 & 1, t0);
-        if (t0 + 1 < t1) load(S, t0 + 1);
-    }
-    __syncthreads();
-    for (int t = t0; t < t1; t++) {
-        // tile t is in LDS buffer t&1; S holds tile t+1 (loaded during the previous
-        // tile): unpack it into the other buffer, start the loads of tile t+2, then
-        // compute tile t.  Storing before computing keeps S's registers free during
-        // the compute phase.
-        if (t + 1 < t1) {
-            store(S, (t + 1) & 1, t + 1);
-            if (t + 2 < t1) load(S, t + 2);
-        }
-        // keep the loads here: left to itself the compiler sinks them next to their
-        // use at the top of the next iteration, exposing their whole latency
-        asm volatile("" ::: "memory");
-        compute(t, t & 1);
+    if (t0 < t1) {      // uniform over the workgroup
+        // tiles from t_mask on may reach past the position of some row of this
+        // workgroup (row q0 of wave 0 is the first): their front takes the masked form
+        const int t_mask = (off + q0 + 1) / BNK;
+        StageK sk;
+        StageV sv;
+        load_k(sk, t0);
+        load_v(sv, t0);
+        store_k(sk, t0 & 1, t0);
+        store_v(sv, t0 & 1, t0);
+        load_k(sk, t0 + 1);
+        store_k(sk, (t0 + 1) & 1, t0 + 1);
+        load_k(sk, t0 + 2);
+        load_v(sv, t0 + 1);
         __syncthreads();
+        Front f = t0 >= t_mask ? front(t0, t0 & 1, std::true_type{}) : front(t0, t0 & 1, std::false_type{});
+        __syncthreads();     // K buffer t0&1 is rewritten in the first iteration
+        auto step = [&](int t, auto mask_tag) {
+            const float pb16 = update(f);
+            store_k(sk, t & 1, t + 2);
+            store_v(sv, (t + 1) & 1, t + 1);
+            load_k(sk, t + 3);
+            load_v(sv, t + 2);
+            // keep the loads here: left to itself the compiler sinks them next to
+            // their use at the top of the next iteration, exposing their latency
+            asm volatile("" ::: "memory");
+            const Front fn = front(t + 1, (t + 1) & 1, mask_tag);
+            back(f.pop, pb16, t & 1);
+            f = fn;
+            __syncthreads();
+        };
+        int t = t0;
+        for (; t + 1 < t1 && t + 1 < t_mask; t++) step(t, std::false_type{});
+        for (; t + 1 < t1; t++) step(t, std::true_type{});
+        back(f.pop, update(f), t & 1);
     }
     if (nsplit == 1) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
