@@ -22,16 +22,19 @@
 // lane always owns one query row:
 //   S^T[key][q] = K·Q^T   A = K codes (x16 unpack), B = the wave's Q codes
 //                         (resident, sign-extended int8); a lane holds query
-//                         q = lane%16 and keys 16t + 4G + r (G = lane/16,
-//                         r = 0..3) of the four 16-key subtiles t.
+//                         q = lane%16 and, in register r of subtile t, key
+//                         16t + 8(G/2) + 2r + G%2 (G = lane/16): the K rows are
+//                         fed in that order, so lane group G holds the even
+//                         (G even) or odd keys of one 8-key group.
 //   O^T[d][q]  = V^T·P^T  B = P straight from those registers (4 dwords: the
 //                         lane's 16 keys), A = V codes laid out in LDS with the
-//                         same key order, so P never leaves the registers.
+//                         same key order, so P never leaves the registers; with
+//                         that order a V operand dword is exactly the x16 even-
+//                         or odd-key bytes of one V cache dword.
 // Row max and row sum over a query's 64 keys are 15 in-lane ops plus two
 // cross-lane steps (xor 16, xor 32).  The workgroup unpacks each K/V tile once
-// into LDS in MFMA operand order (K: x16 bytes per (subtile, k-step, lane);
-// V: v_perm of the x16 bytes into [r0 r2 r1 r3] per 4 keys), so the waves only
-// issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
+// into LDS in MFMA operand order (x16 bytes per (subtile, k-step, lane)), so the
+// waves only issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.
 #include <type_traits>
@@ -53,6 +56,11 @@ constexpr int KU_BYTES = 4 * 4 * 64 * 16;   // unpacked K operands of one tile
 constexpr int VU_BYTES = 16 * 64 * 16;      // unpacked V operands of one tile
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Key order within a 16-key subtile: output register r of lane group G holds key
+// key_of_slot(G, r); the K row fed to the MFMA at slot 4G + r is that key.
+__device__ __forceinline__ int key_of_slot(int G, int r) { return 8 * (G >> 1) + 2 * r + (G & 1); }
+__device__ __forceinline__ int slot_of_key(int k) { return 4 * (2 * (k >> 3) + (k & 1)) + ((k & 7) >> 1); }
 
 // Products x[4G + r] * y for r = 0..3 in the 16x16 accumulator layout (lane l =
 // 16G + i holds rows 4G..4G+3 of column i), on the matrix core: v_mfma_f32_4x4x1
@@ -292,6 +300,10 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 
     const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
     const int qi = lane & 15, G = lane >> 4;
+    // the key (within a subtile) whose scale this lane supplies to the scale products:
+    // outer4 gives lane l, output r, the operand of lane 4(l/4) + r, i.e. of register r
+    // of lane group G
+    const int kslot = key_of_slot(G, lane & 3);
     const int head = blockIdx.y, vh = head / ratio;
     const int q0 = blockIdx.x * QROWS;
     const int qrow = q0 + 16 * w + qi;
@@ -382,8 +394,8 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         S.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_vs, tid * 4, t * HD * 4, 0));
     };
     auto store_k = [&](const StageK& S, int b, int t) {
-        // x16 bytes of dwords (8p + 2G, 8p + 2G + 1) for lane G*16 + kk%16 of subtile kk/16;
-        // keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
+        // x16 bytes of dwords (8p + 2g, 8p + 2g + 1) for lane g*16 + slot of kk%16 in
+        // subtile kk/16; keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
         unsigned char* kub = ku + b * KU_BYTES;
         const int kk = tid & 63, p = tid >> 6;
         const uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
@@ -391,13 +403,15 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         for (int g = 0; g < 4; g++) {
             const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
                                        odd_x16(d[2 * g + 1]));
-            *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + (kk & 15)) * 16) = v;
+            *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + slot_of_key(kk & 15)) * 16) = v;
         }
         if (tid < 2 * BNK) ks_l[b][tid] = t * BNK + (tid & 63) < kv_cap ? S.ks : 1.f;
     };
     auto store_v = [&](const StageV& S, int b, int t) {
-        // lane G*16 + d%16 of dim tile d/16 gets keys 16t + 4G + {0,2,1,3}, t = 0..3;
-        // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152)
+        // lane G*16 + d%16 of dim tile d/16 gets, in dword t = 0..3, the x16 bytes of
+        // the even (G even) or odd keys of 8-key group 2t + G/2 -- keys
+        // 16t + key_of_slot(G, r), r = 0..3, as P holds them; a group of 8 keys is
+        // read only if it is whole (flash_attn_core.h:150-152)
         unsigned char* vub = vu + b * VU_BYTES;
         uint32_t e[8], o[8];
 #pragma unroll
@@ -406,14 +420,10 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             o[g] = odd_x16(S.v[g]);
         }
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint32_t sel = (g & 1) ? 0x07060302u : 0x05040100u;
-            uint4 v;
-            v.x = __builtin_amdgcn_perm(o[0 + (g >> 1)], e[0 + (g >> 1)], sel);
-            v.y = __builtin_amdgcn_perm(o[2 + (g >> 1)], e[2 + (g >> 1)], sel);
-            v.z = __builtin_amdgcn_perm(o[4 + (g >> 1)], e[4 + (g >> 1)], sel);
-            v.w = __builtin_amdgcn_perm(o[6 + (g >> 1)], e[6 + (g >> 1)], sel);
-            *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + g * 16 + (tid & 15)) * 16) = v;
+        for (int G = 0; G < 4; G++) {
+            const uint32_t* src = (G & 1) ? o : e;
+            const uint4 v = make_uint4(src[G >> 1], src[2 + (G >> 1)], src[4 + (G >> 1)], src[6 + (G >> 1)]);
+            *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + G * 16 + (tid & 15)) * 16) = v;
         }
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
     };
@@ -441,8 +451,8 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
             a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
             // key scale x query scale of each entry, then S = a1 * c1 + a0 * c0
-            const v4f c0 = outer4(ksb[16 * kt + 4 * G + (lane & 3)], A0);
-            const v4f c1 = outer4(ksb[BNK + 16 * kt + 4 * G + (lane & 3)], A1);
+            const v4f c0 = outer4(ksb[16 * kt + kslot], A0);
+            const v4f c1 = outer4(ksb[BNK + 16 * kt + kslot], A1);
 #pragma unroll
             for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[r], (float)a0[r] * c0[r]);
         }
@@ -452,7 +462,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        if (kb + 16 * kt + 4 * G + r > off + qrow) sv[kt][r] = -__builtin_inff();
+                        if (kb + 16 * kt + key_of_slot(G, r) > off + qrow) sv[kt][r] = -__builtin_inff();
             }
         }
         // ---- tile row max over the 64 keys of this lane's query
@@ -490,7 +500,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m) * 7.f;
                 pq[r] = (int)(p + 0.5f);
             }
-            pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[2] << 8 | (uint32_t)pq[1] << 16 | (uint32_t)pq[3] << 24;
+            pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[1] << 8 | (uint32_t)pq[2] << 16 | (uint32_t)pq[3] << 24;
         }
         Front f;
         f.pop = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
