@@ -133,7 +133,7 @@ __device__ __forceinline__ void quant_lane(const float4 (&x)[8], uint4& a0, uint
 template <int M, int GPW>
 constexpr int gemv_al_bytes() { return M * GPW * 8 * 16; }
 
-template <int M, int GPW, int RB, bool AL, bool GSUM, bool QIN>
+template <int M, int GPW, int RB, bool AL, bool GSUM, bool QIN, bool HS>
 __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
                                                     const int8_t* __restrict__ xq,
@@ -148,6 +148,7 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     constexpr int ACH = M * GPW * 8;             // AL: 16-byte chunks of a wave's activations
     constexpr int AIN = (ACH + 63) / 64;         // AL: load instructions for them
     static_assert(!AL || (RB == 1 && !QIN), "line-wise activation loads: one row block, int8 input");
+    static_assert(!HS || (AL && GPW == 2), "hoisted scales: line-wise loads, one group pair per wave");
     extern __shared__ __align__(16) unsigned char smem[];
     const int W = blockDim.x >> 6;
     const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
@@ -191,6 +192,19 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
     }
     const int jr = j % M, jg = j / M;
     const v4i zero = {0, 0, 0, 0};
+    // HS (even NG, at most 8 chunks per wave): the scale dword (groups 2c, 2c+1) of
+    // row n0 + j at this wave's iterations q and q + 4, loaded once before the loop;
+    // iteration it takes it from lane j + 16 (it % 4).  Iterations past the wave's
+    // last read chunk c_lo again (in bounds, unused).
+    uint32_t hsc[2] = {0u, 0u};
+    if constexpr (HS) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            int c = c_lo + w + (q + 4 * i) * W;
+            c = c < c_hi ? c : c_lo;
+            hsc[i] = *reinterpret_cast<const uint32_t*>(ws + (size_t)rj[0] * NG + 2 * c);
+        }
+    }
 
     float yacc[RB][M];
 #pragma unroll
@@ -198,13 +212,14 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
 #pragma unroll
         for (int r = 0; r < M; r++) yacc[rb][r] = 0.f;
 
-    for (int c = c_lo + w; c < c_hi; c += W) {
+    int it = 0;
+    for (int c = c_lo + w; c < c_hi; c += W, it++) {
         const int g0 = uniform(c * GPW);
         // (1) this wave's scales: RB x 16 rows x GPW fp16, as dwords (even NG:
         //     every row starts 4-byte aligned) or as halves (odd NG)
         uint32_t sw[RB][(GPW / 2 + 3) / 4];
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+        for (int rb = 0; rb < (HS ? 0 : RB); rb++)
 #pragma unroll
             for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
                 const int dw = q + 4 * d;
@@ -275,7 +290,7 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
             }
         }
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+        for (int rb = 0; rb < (HS ? 0 : RB); rb++)
 #pragma unroll
             for (int d = 0; d < (GPW / 2 + 3) / 4; d++) {
                 const int dw = q + 4 * d;
@@ -377,7 +392,10 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
                         if (GSUM && lane < 16 && nl < N)
 #pragma unroll
                             for (int r = 0; r < M; r++) gsum[((size_t)r * N + nl) * NG + g] = acc[r] >> 4;
-                        const uint32_t pair = wsl[(rb * 16 + j) * (GPW / 2) + p];
+                        const uint32_t pair =
+                            HS ? (uint32_t)__builtin_amdgcn_ds_bpermute((j + 16 * (it & 3)) * 4,
+                                                                        (int)((it & 4) ? hsc[1] : hsc[0]))
+                               : wsl[(rb * 16 + j) * (GPW / 2) + p];
                         const float s16 = f16_bits_to_f32((uint16_t)(h ? pair >> 16 : pair & 0xFFFFu)) * 0.0625f;
 #pragma unroll
                         for (int r = 0; r < M; r++) yacc[rb][r] = fmaf((float)acc[r], s16 * a_s[r], yacc[rb][r]);
@@ -461,12 +479,24 @@ hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_
     // default 64 KB of dynamic LDS
     if constexpr (RB == 1 && !QIN) {
         if (base + al <= 65536) {
-            hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, true, GSUM, QIN>), dim3(grid), dim3(64 * waves), base + al,
-                               st, wq, ws, xq, sa, xf, y, gsum, N, K, sp);
+            // Scales hoisted out of the chunk loop where a wave has at least 3 and at
+            // most 8 chunks and the tile has at most 4 waves (measured: gate/up, 4
+            // waves x 5 chunks, 11.42 -> 11.30 us; with 16 waves, as at the down and
+            // M=1 shapes, the extra loads cost more than they save).
+            const int NG = K / kGroup, NC = (NG + GPW - 1) / GPW, per_wave = (NC + waves - 1) / waves;
+            if constexpr (GPW == 2) {
+                if (!(NG & 1) && waves <= 4 && per_wave >= 3 && per_wave <= 8) {
+                    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, true, GSUM, QIN, true>), dim3(grid),
+                                       dim3(64 * waves), base + al, st, wq, ws, xq, sa, xf, y, gsum, N, K, sp);
+                    return hipGetLastError();
+                }
+            }
+            hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, true, GSUM, QIN, false>), dim3(grid), dim3(64 * waves),
+                               base + al, st, wq, ws, xq, sa, xf, y, gsum, N, K, sp);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, false, GSUM, QIN>), dim3(grid), dim3(64 * waves), base, st, wq, ws,
+    hipLaunchKernelGGL((gemv_w4a8_k<M, GPW, RB, false, GSUM, QIN, false>), dim3(grid), dim3(64 * waves), base, st, wq, ws,
                        xq, sa, xf, y, gsum, N, K, sp);
     return hipGetLastError();
 }
