@@ -488,10 +488,14 @@ def main() -> int:
     g_, w_, rb_ = plan["groups_per_wave"], plan["waves"], plan["row_blocks"]
     # line-wise activation loads: one row block and their LDS slices within 64 KB (the launcher's rule)
     al = rb_ == 1 and w_ * 16 * g_ * 2 + w_ * M * 16 * 4 + w_ * M * g_ * 8 * 16 <= 65536
+    # scales hoisted out of the chunk loop: 2 groups per wave, even K/128, 3-8 chunks per wave, <= 4 waves
+    ng_gu = Kgu // 128
+    per_wave = -(-(-(-ng_gu // g_)) // w_)
+    hs = al and g_ == 2 and ng_gu % 2 == 0 and w_ <= 4 and 3 <= per_wave <= 8
     # measured ceiling: the fastest single launch that reads the same byte count
     from rt4_amd import probe
     ceil_gu = probe.read_ceiling(torch, gu_bytes, timed_graph=timed_graph)
-    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false> "
+    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false,{str(hs).lower()}> "
                           f"(gate/up GEMV, "
                           f"M={M} K={Kgu} N={Ngu}, "
                           f"{plan['waves']} waves/tile, {plan['k_splits']} K pieces/leftover tile)",
