@@ -123,6 +123,25 @@ def test_gemv_every_config(rt4, orc, torch_gpu, gpw, waves):
     assert rel_l2(host(y), ref) < TIGHT
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("waves,splits", [(2, 1), (3, 1), (4, 1), (4, 4)])
+def test_gemv_hoisted_scales(rt4, orc, torch_gpu, M, waves, splits):
+    """Two groups per wave with 3-8 chunks per wave and at most 4 waves: the launch
+    that loads each wave's weight scales once before its chunk loop (K = 3072: 12
+    chunks; with 4 K-pieces per leftover tile a piece's waves have fewer chunks
+    than the scale registers cover)."""
+    N, K = 4100, 3072
+    print(f"case gemv_hs M={M} waves={waves} splits={splits}", flush=True)
+    c, wq, ws, x = _gemv_inputs(torch_gpu, 15, M, N, K)
+    xq, sa = rt4.quant_act_a8(x)
+    y = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=2, waves=waves, k_splits=splits)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=2, waves=waves, k_splits=splits)
+    torch_gpu.cuda.synchronize()
+    ref = orc.gemv_w4a8(c["wq"], c["ws"], c["x"])
+    assert rel_l2(host(y), ref) < TIGHT
+    assert torch_gpu.equal(y, y2)
+
+
 @pytest.mark.parametrize("M,N,K,splits", [(4, 300, 3072, 8), (1, 300, 3072, 64), (4, 4176, 8192, 1),
                                            (4, 4176, 8192, 2), (2, 4176, 8192, 5), (3, 4176, 8192, 64),
                                            (4, 4176, 8192, 0), (1, 4100, 17408, 0)])
