@@ -36,7 +36,10 @@
 // into LDS in MFMA operand order (x16 bytes per (subtile, k-step, lane)), so the
 // waves only issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
-// which leaves its state bit-for-bit unchanged.
+// which leaves its state bit-for-bit unchanged.  The tile loop is a two-tile
+// pipeline (S and P of the next tile beside the PV product of the current one;
+// see the loop), the scale products of both contractions run on
+// v_mfma_f32_4x4x1f32, and K/V are read with range-checked buffer loads.
 #include <type_traits>
 
 #include "rt4_dev.h"
