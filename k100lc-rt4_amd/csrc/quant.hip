@@ -40,33 +40,47 @@ __device__ __forceinline__ uint2 interleave8(const int c[8]) {
 // Outputs: xq int8 [rows][K] interleaved, sa f32 [rows][K/128], and optionally
 // asu = Σq per group (the reference needs it for its u=code+8 correction; the
 // MFMA GEMV here does not, but it is kept for parity checks).
+// x/s: for a wave whose scales all lie in [2^-96, 2^100], a correctly rounded
+// reciprocal y = 1/s and one Markstein correction, t = RN(x*y),
+// q = RN(t + RN(x - t*s)*y) with the residual exact by FMA, which for y = RN(1/s)
+// and no underflow is the correctly rounded quotient (Markstein's theorem), i.e.
+// bit-equal to x/s; other waves (tiny or non-finite groups) divide.
+// ALIGNED: x rows 16-byte aligned (vector loads); SUMS: asu is written.
 // grid (ceil(K/8/256), rows), block 256.
+template <bool ALIGNED, bool SUMS>
 __global__ __launch_bounds__(256) void quant_act_a8_k(const float* __restrict__ x,
                                                       int8_t* __restrict__ xq,
                                                       float* __restrict__ sa,
-                                                      int32_t* __restrict__ asu, int K,
-                                                      int x_aligned) {
+                                                      int32_t* __restrict__ asu, int K) {
     const int m = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;  // 8-element block in the row
     if (i >= (K >> 3)) return;                     // K%128==0: whole 16-lane runs exit together
     float v[8];
-    load8(x + (size_t)m * K + 8 * (size_t)i, x_aligned, v);
+    load8(x + (size_t)m * K + 8 * (size_t)i, ALIGNED, v);
     float amax = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
     amax = run_max<16>(amax);
     const float s = amax > 0.f ? amax / 127.f : 1.f;
     int c[8];
-    int part = 0;
+    if (__all(s >= 0x1p-96f && s <= 0x1p+100f)) {
+        const float y = 1.f / s;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        c[e] = clampi((int)lrintf(v[e] / s), -128, 127);
-        part += c[e];
+        for (int e = 0; e < 8; e++) {
+            const float t = v[e] * y;
+            c[e] = clampi((int)lrintf(fmaf(fmaf(-t, s, v[e]), y, t)), -128, 127);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) c[e] = clampi((int)lrintf(v[e] / s), -128, 127);
     }
     *reinterpret_cast<uint2*>(xq + (size_t)m * K + 8 * (size_t)i) = interleave8(c);
     const int NG = K >> 7;
     if ((i & 15) == 0) sa[(size_t)m * NG + (i >> 4)] = s;
-    if (asu) {
+    if constexpr (SUMS) {
+        int part = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) part += c[e];
         part = run_sum<16>(part);
         if ((i & 15) == 0) asu[(size_t)m * NG + (i >> 4)] = part;
     }
@@ -75,8 +89,15 @@ __global__ __launch_bounds__(256) void quant_act_a8_k(const float* __restrict__ 
 hipError_t launch_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows,
                                int K, hipStream_t st) {
     const dim3 grid((K / 8 + 255) / 256, rows);
-    const int aligned = ((uintptr_t)x & 15) == 0;
-    hipLaunchKernelGGL(quant_act_a8_k, grid, dim3(256), 0, st, x, xq, sa, asu, K, aligned);
+    const bool aligned = ((uintptr_t)x & 15) == 0;
+    if (aligned && !asu)
+        hipLaunchKernelGGL((quant_act_a8_k<true, false>), grid, dim3(256), 0, st, x, xq, sa, asu, K);
+    else if (aligned)
+        hipLaunchKernelGGL((quant_act_a8_k<true, true>), grid, dim3(256), 0, st, x, xq, sa, asu, K);
+    else if (!asu)
+        hipLaunchKernelGGL((quant_act_a8_k<false, false>), grid, dim3(256), 0, st, x, xq, sa, asu, K);
+    else
+        hipLaunchKernelGGL((quant_act_a8_k<false, true>), grid, dim3(256), 0, st, x, xq, sa, asu, K);
     return hipGetLastError();
 }
 
