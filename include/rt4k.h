@@ -217,7 +217,8 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
  * online rescaling.  Query row i has position off + i.  Replaces the prefill
  * branch of k_attention (src/kernels.h:81, src/k_fa.hip:282-300; kernel fa_int4,
  * kernels/flash_attn_core.h:74-435).  n_q % 64 == 0, kv_cap % 64 == 0,
- * n_tile * 64 <= kv_cap; BG of the V cache must be 64. */
+ * n_tile * 64 <= kv_cap, kv_cap <= 16777152 (2^24 - 64: one KV head's cache is
+ * addressed with 32-bit offsets); BG of the V cache must be 64. */
 int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
                           const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv,
                           int off, int n_tile, int n_heads, int ratio, int kv_cap, void* stream);

@@ -641,15 +641,20 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
                       "k_kv_append_v launch");
 }
 
+// The prefill kernel addresses one KV head's cache through 32-bit buffer offsets
+// (kv_cap * 128 bytes of K codes, plus up to three tiles read past the end).
+constexpr int kMaxKvCap = (1 << 24) - 64;
+
 int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
                               const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
                               int n_tile, int n_heads, int ratio, int kv_cap, int kv_splits, void* stream) {
     if (!out || !qq || !qsc || !kc || !ksc || !vc || !vsc) return fail(RT4_E_ARG, "k_attention: null pointer");
     if (n_q < 64 || n_q % 64 || n_kv < 1 || n_kv > kv_cap || off < 0 || kv_cap % 64 || n_tile < 1 ||
         (long long)n_tile * 64 > kv_cap || n_heads < 1 || ratio < 1 || n_heads % ratio || n_q > 65535 * 64 ||
-        n_heads > 65535)
+        n_heads > 65535 || kv_cap > kMaxKvCap)
         return fail(RT4_E_SHAPE,
-                    "k_attention: n_q=%d (multiple of 64) n_kv=%d off=%d n_tile=%d n_heads=%d ratio=%d kv_cap=%d",
+                    "k_attention: n_q=%d (multiple of 64) n_kv=%d off=%d n_tile=%d n_heads=%d ratio=%d kv_cap=%d "
+                    "(at most 16777152)",
                     n_q, n_kv, off, n_tile, n_heads, ratio, kv_cap);
     if (kv_splits < 0 || kv_splits > 64) return fail(RT4_E_ARG, "k_attention: kv_splits=%d (0..64)", kv_splits);
     if (!aligned(qq, 16) || !aligned(kc, 16) || !aligned(vc, 4) || !aligned(out, 16) || !aligned(qsc, 4) ||

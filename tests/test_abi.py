@@ -176,6 +176,17 @@ def test_gemm_rejects_shapes_beyond_32bit_offsets(rt4, M, N, K):
     assert L.rt4_gemm_w4a8_i8(W16, ctypes.c_void_p(0x1004), W16, W16, W16, 838860, 64, 5120, None) == 2
 
 
+def test_attention_rejects_caches_beyond_32bit_offsets(rt4):
+    """One KV head's cache is addressed with 32-bit buffer offsets (kv_cap * 128 bytes
+    of K codes): kv_cap above 2^24 - 64 is refused before any device work."""
+    L = rt4.lib()
+    P = ctypes.c_void_p(0x10000)
+    args = lambda cap: (P, P, P, P, P, P, P, 64, 64, 0, 1, 8, 1, cap, 0, None)  # noqa: E731
+    assert L.rt4_attention_prefill_cfg(*args(1 << 24)) == 1          # RT4_E_SHAPE
+    assert "kv_cap" in L.rt4_last_error().decode()
+    assert L.rt4_attention_prefill_cfg(*args((1 << 24) + 64)) == 1
+
+
 def test_noalloc_gemv_rejects_beyond_its_static_scratch(rt4):
     """rt4_gemv_w4a8_noalloc has a fixed scratch (K <= 65536); larger K is an error, not an allocation."""
     L = rt4.lib()
