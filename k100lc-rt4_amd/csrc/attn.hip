@@ -99,7 +99,7 @@ __device__ __forceinline__ uint32_t code4(float x, float s) {
 // Q of all heads (restates attn_q_quant_k, src/k_new.hip:228-253): x f32 [T][H][D]
 // -> qq [H][TP][D/8], qs [H][D/G][TP].  One lane per 8 elements; a G-group is GL =
 // G/8 consecutive lanes.  Rows >= T are not written.
-template <int GL>
+template <int GL, bool ALIGNED>
 __global__ __launch_bounds__(256) void attn_q_quant_k(uint32_t* __restrict__ qq, float* __restrict__ qs,
                                                       const float* __restrict__ x, int T, int H, int D, int TP) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -109,16 +109,27 @@ __global__ __launch_bounds__(256) void attn_q_quant_k(uint32_t* __restrict__ qq,
     const int rh = (int)(i / dw), h = rh % H, r = rh / H;
     const float* xr = x + (size_t)rh * D + 8 * e8;  // (r*H + h)*D
     float v[8], amax = 0.f;
+    if (ALIGNED) {
+        const float4 a = reinterpret_cast<const float4*>(xr)[0], b = reinterpret_cast<const float4*>(xr)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        v[e] = xr[e];
-        amax = fmaxf(amax, fabsf(v[e]));
+        for (int e = 0; e < 8; e++) v[e] = xr[e];
     }
+#pragma unroll
+    for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
     amax = run_max<GL>(amax);
     const float s = amax > 0.f ? amax / 7.f : 1.f;
     uint32_t w = 0;
+    if (__all(recip_div_ok(s))) {   // x / s through the reciprocal (bit-equal)
+        const float y = 1.f / s;
 #pragma unroll
-    for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
+        for (int e = 0; e < 8; e++)
+            w |= ((uint32_t)clampi((int)lrintf(div_by_recip(v[e], s, y)), -8, 7) & 0xFu) << (4 * e);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
+    }
     qq[((size_t)h * TP + r) * dw + e8] = w;
     const int ng = D / (8 * GL);
     if (e8 % GL == 0) qs[((size_t)h * ng + e8 / GL) * TP + r] = s;
@@ -645,12 +656,19 @@ hipError_t launch_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, i
     const size_t n = (size_t)T * H * (D / 8);
     if (n == 0) return hipSuccess;
     const dim3 grid((unsigned)((n + 255) / 256));
+    // rows of D (a multiple of 8) floats: every lane's 8 elements are 32-byte aligned
+    // when x is 16-byte aligned
+    const bool al = ((uintptr_t)x & 15) == 0;
+#define RT4_QQ(GLV)                                                                                        \
+    if (al) hipLaunchKernelGGL((attn_q_quant_k<GLV, true>), grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); \
+    else hipLaunchKernelGGL((attn_q_quant_k<GLV, false>), grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP);
     switch (G / 8) {
-        case 8: hipLaunchKernelGGL(attn_q_quant_k<8>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
-        case 16: hipLaunchKernelGGL(attn_q_quant_k<16>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
-        case 32: hipLaunchKernelGGL(attn_q_quant_k<32>, grid, dim3(256), 0, st, qq, qs, x, T, H, D, TP); break;
+        case 8: RT4_QQ(8) break;
+        case 16: RT4_QQ(16) break;
+        case 32: RT4_QQ(32) break;
         default: return hipErrorInvalidValue;
     }
+#undef RT4_QQ
     return hipGetLastError();
 }
 

@@ -63,13 +63,10 @@ __global__ __launch_bounds__(256) void quant_act_a8_k(const float* __restrict__ 
     amax = run_max<16>(amax);
     const float s = amax > 0.f ? amax / 127.f : 1.f;
     int c[8];
-    if (__all(s >= 0x1p-96f && s <= 0x1p+100f)) {
+    if (__all(recip_div_ok(s))) {
         const float y = 1.f / s;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float t = v[e] * y;
-            c[e] = clampi((int)lrintf(fmaf(fmaf(-t, s, v[e]), y, t)), -128, 127);
-        }
+        for (int e = 0; e < 8; e++) c[e] = clampi((int)lrintf(div_by_recip(v[e], s, y)), -128, 127);
     } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) c[e] = clampi((int)lrintf(v[e] / s), -128, 127);
@@ -126,9 +123,18 @@ __global__ __launch_bounds__(256) void quant_rows_a8_k(
     const float s = amax > 0.f ? amax / 119.f : 1.f;
     uint32_t wh = 0, wl = 0;
     int c[8];
+    float qv[8];   // x / s: through the reciprocal when the wave's scales allow (bit-equal)
+    if (__all(recip_div_ok(s))) {
+        const float y = 1.f / s;
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[e] = div_by_recip(v[e], s, y);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) qv[e] = v[e] / s;
+    }
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const int q8 = clampi((int)lrintf(v[e] / s), -128, 119);
+        const int q8 = clampi((int)lrintf(qv[e]), -128, 119);
         const int h = (q8 + 8) >> 4;  // floor, also for negatives
         const int l = q8 - 16 * h;    // in [-8, 7]
         wh |= (uint32_t)(h & 0xF) << (4 * e);

@@ -51,6 +51,18 @@ __device__ __forceinline__ uint32_t odd_x16(uint32_t w) { return w & 0xF0F0F0F0u
 // Saturating helpers for the quantizers (same clamp order as the reference).
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v > hi ? hi : (v < lo ? lo : v); }
 
+// x / s rounded to nearest through the reciprocal: with y = RN(1/s) (hipcc's
+// division is correctly rounded), t = RN(x*y) and the residual x - t*s exact by
+// FMA, RN(t + residual*y) is the correctly rounded quotient whenever nothing
+// underflows (Markstein's theorem), i.e. bit-equal to x / s.  The quantizers take
+// this path only when every scale of the wave lies in [2^-96, 2^100]; tiny or
+// non-finite scales divide.
+__device__ __forceinline__ bool recip_div_ok(float s) { return s >= 0x1p-96f && s <= 0x1p+100f; }
+__device__ __forceinline__ float div_by_recip(float x, float s, float y) {
+    const float t = x * y;
+    return fmaf(fmaf(-t, s, x), y, t);
+}
+
 // Agent-coherent (sc1) 4-byte vector store / load of split-tile partials, each
 // with its wait in the same asm statement: the store has reached the coherent
 // level before the counter increment that publishes it, and the load's value is
