@@ -91,6 +91,20 @@ __device__ __forceinline__ uint2 codes_i8(uint32_t w) {
 __device__ __forceinline__ uint32_t code4(float x, float s) {
     return (uint32_t)clampi((int)lrintf(x / s), -8, 7) & 0xFu;
 }
+// The codes of 8 values as one dword (value e in nibble e), x / s taken through
+// the reciprocal when every scale of the wave allows it (bit-equal to code4).
+__device__ __forceinline__ uint32_t codes8(const float* v, float s) {
+    uint32_t w = 0;
+    if (__all(recip_div_ok(s))) {
+        const float y = 1.f / s;
+#pragma unroll
+        for (int e = 0; e < 8; e++) w |= ((uint32_t)clampi((int)lrintf(div_by_recip(v[e], s, y)), -8, 7) & 0xFu) << (4 * e);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
+    }
+    return w;
+}
 
 }  // namespace
 
@@ -120,16 +134,7 @@ __global__ __launch_bounds__(256) void attn_q_quant_k(uint32_t* __restrict__ qq,
     for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
     amax = run_max<GL>(amax);
     const float s = amax > 0.f ? amax / 7.f : 1.f;
-    uint32_t w = 0;
-    if (__all(recip_div_ok(s))) {   // x / s through the reciprocal (bit-equal)
-        const float y = 1.f / s;
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            w |= ((uint32_t)clampi((int)lrintf(div_by_recip(v[e], s, y)), -8, 7) & 0xFu) << (4 * e);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
-    }
+    const uint32_t w = codes8(v, s);
     qq[((size_t)h * TP + r) * dw + e8] = w;
     const int ng = D / (8 * GL);
     if (e8 % GL == 0) qs[((size_t)h * ng + e8 / GL) * TP + r] = s;
@@ -156,10 +161,7 @@ __global__ __launch_bounds__(256) void kv_append_k_k(uint32_t* __restrict__ kc, 
     }
     amax = run_max<GL>(amax);
     const float s = amax > 0.f ? amax / 7.f : 1.f;
-    uint32_t w = 0;
-#pragma unroll
-    for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
-    kc[((size_t)h * kv_total + kv) * dw + e8] = w;
+    kc[((size_t)h * kv_total + kv) * dw + e8] = codes8(v, s);
     const int ng = D / (8 * GL);
     if (e8 % GL == 0) ksc[((size_t)h * ng + e8 / GL) * kv_total + kv] = s;
 }
@@ -266,12 +268,7 @@ __global__ __launch_bounds__(256) void kv_append_v64_k(uint32_t* __restrict__ vc
     if (p == 0) vsc[((size_t)h * (kv_total / BG) + tile) * D + d] = s;
     uint32_t* out = vc + ((size_t)h * (kv_total / 8) + (size_t)tile * (BG / 8)) * D + d;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) w |= code4(v[8 * j + e], s) << (4 * e);
-        out[(size_t)(2 * p + j) * D] = w;
-    }
+    for (int j = 0; j < 2; j++) out[(size_t)(2 * p + j) * D] = codes8(v + 8 * j, s);
 }
 
 // Phase 2 for BG = 64: wave p restores slots 16p..16p+15 (see kv_stage_v_k).
