@@ -293,6 +293,30 @@ def test_feeders_bit_exact(rt4, orc, torch_gpu, T, n_kv, H, KVH, steps):
 
 
 @pytest.mark.gpu
+def test_q_quant_unaligned_input(rt4, orc, torch_gpu):
+    """Q rows that are not 16-byte aligned (the scalar-load instance of the Q
+    quantizer): codes and scales bit-identical to the oracle, tiny and zero groups
+    included (they take the division path)."""
+    print("case attn_q_quant unaligned", flush=True)
+    torch = torch_gpu
+    rng = np.random.default_rng(21)
+    T, H = 70, 3
+    q = rng.standard_normal((T, H, HD)).astype(np.float32)
+    q[0, 0, :128] = 0.0
+    q[1, 1, 128:] *= np.float32(1e-30)
+    TP = (T + 63) // 64 * 64
+    buf = torch.empty(T * H * HD + 1, dtype=torch.float32, device="cuda")
+    qd = buf[1:].view(T, H, HD)
+    qd.copy_(dev(torch, q))
+    assert qd.data_ptr() % 16 != 0
+    qq, qs = rt4.attn_q_quant(qd, TP)
+    c = [np.zeros((H, TP, 32), np.uint32), np.ones((H, 2, TP), np.float32)]
+    orc.attn_q_quant(q, TP, qq=c[0], qs=c[1])
+    assert np.array_equal(host(qq).view(np.uint32), c[0])
+    assert np.array_equal(host(qs).view(np.uint32), c[1].view(np.uint32))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("BG,D", [(32, 256), (64, 200), (128, 256)])
 def test_kv_append_v_other_tiles(rt4, orc, torch_gpu, BG, D):
     """V tiles other than 64 keys (the generic kernels) and a dim count that is not

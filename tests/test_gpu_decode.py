@@ -55,6 +55,24 @@ def test_quant_act_bit_exact(rt4, orc, torch_gpu, M, K):
     assert np.array_equal(host(asu), asu_o)
 
 
+def test_quant_act_unaligned_with_sums(rt4, orc, torch_gpu):
+    """Input rows not 16-byte aligned, group sums wanted: the scalar-load instance
+    with sums, bit-identical to the oracle (edge values included)."""
+    M, K = 3, 2048
+    print(f"case quant_act unaligned M={M} K={K}", flush=True)
+    x = edge_acts(np.random.default_rng(301), M, K)
+    buf = torch_gpu.empty(M * K + 1, dtype=torch_gpu.float32, device="cuda")
+    xd = buf[1:].view(M, K)
+    xd.copy_(dev(torch_gpu, x))
+    assert xd.data_ptr() % 16 != 0
+    xq, sa, asu = rt4.quant_act_a8(xd, want_sums=True)
+    torch_gpu.cuda.synchronize()
+    q, sa_o, asu_o = orc.quant_act(x)
+    assert np.array_equal(layout.deinterleave(host(xq)), q)
+    assert np.array_equal(host(sa).view(np.uint32), sa_o.view(np.uint32))
+    assert np.array_equal(host(asu), asu_o)
+
+
 def _gemv_inputs(torch, seed, M, N, K):
     c = workload.gemv_case(seed, M, N, K)
     return c, dev(torch, c["wq"]), dev(torch, c["ws"]), dev(torch, c["x"])
