@@ -40,7 +40,10 @@
 // * Weight scales: each wave loads its 16 rows x GPW fp16 scales as dwords into
 //   a private LDS slice.  Scales and activations are issued before the weight
 //   stream: vmcnt retires in order, so the first group can start as soon as its
-//   weights land.
+//   weights land.  With 2 groups per wave, 3-8 chunks per wave and at most 4
+//   waves (HS), each lane instead loads the scale dwords of two of its wave's
+//   chunks once, before the chunk loop, and each chunk takes its dword from the
+//   right lane with one ds_bpermute.
 // * fp32 fold once per group: fp32(16I) * (f16(ws)/16 * sa) equals the
 //   reference's (ws*sa)*I term bit for bit (power-of-two scaling is exact); only
 //   the order of the sum over groups differs from the reference.  The W partial

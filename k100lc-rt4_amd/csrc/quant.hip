@@ -1,9 +1,10 @@
 // quant.hip -- activation quantizers of the RT4 path, gfx950.
 //
 // Three reference quantizers are restated here; each must produce bit-identical
-// integer codes and scales, so every step uses the same IEEE single operations
-// as the reference (correctly rounded division -- hipcc's default -- and
-// round-half-to-even lrintf).  One lane owns 8 consecutive elements of a row,
+// integer codes and scales, so every step computes the same IEEE single results
+// as the reference: the correctly rounded quotient x/s (hipcc's division, or the
+// reciprocal form of rt4_dev.h's div_by_recip, which equals it wherever a wave
+// takes it) and round-half-to-even lrintf.  One lane owns 8 consecutive elements of a row,
 // so a G-element group is an aligned run of G/8 lanes and its max-abs is a
 // short xor-shuffle reduction; loads and stores are full dwords.
 #include "rt4_dev.h"
