@@ -227,7 +227,9 @@ int rt4_attention_prefill(float* out, const uint32_t* qq, const float* qsc, cons
  * (tuning and tests; 0 selects the default that balances the grid over the
  * device's CUs).  With more than one split each split writes its partial state
  * (unnormalised output, running max, denominator) to library scratch (grown
- * with hipMalloc) and a second kernel combines the splits in order. */
+ * with hipMalloc, with one counter per (query block, head)), and the split that
+ * finishes last for a (query block, head) combines them in split order within
+ * the same launch. */
 int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
                               const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv,
                               int off, int n_tile, int n_heads, int ratio, int kv_cap, int kv_splits,

@@ -58,6 +58,7 @@ constexpr float L2E = 1.4426950408889634f;
 constexpr int KU_BYTES = 4 * 4 * 64 * 16;   // unpacked K operands of one tile
 constexpr int VU_BYTES = 16 * 64 * 16;      // unpacked V operands of one tile
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Key order within a 16-key subtile: output register r of lane group G holds key
@@ -303,11 +304,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                                                     const float* __restrict__ vsc, float* __restrict__ out,
                                                     int n_q, int n_kv, int off, int n_tile, int ratio,
                                                     int kv_cap, int nsplit, float* __restrict__ opart,
-                                                    float2* __restrict__ mlpart) {
+                                                    float2* __restrict__ mlpart, int* __restrict__ cnt) {
     __shared__ __align__(16) unsigned char ku[2 * KU_BYTES];   // x2: [subtile][k-step][lane] x 16 B
     __shared__ __align__(16) unsigned char vu[2 * VU_BYTES];   // x2: [dim tile][lane] x 16 B
     __shared__ __align__(16) float ks_l[2][2 * BNK];
     __shared__ __align__(16) float vs_l[2][HD];
+    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
     const int qi = lane & 15, G = lane >> 4;
@@ -602,48 +604,86 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             *reinterpret_cast<float4*>(orow + 16 * dt) =
                 make_float4(O[dt][0] * inv, O[dt][1] * inv, O[dt][2] * inv, O[dt][3] * inv);
     } else {
-        // partial state of this split: unnormalised O, running max (log2 units), L
-        const size_t prow = ((size_t)split * gridDim.y + head) * n_q + qrow;
-        float* orow = opart + prow * HD + 4 * G;
+        // Split-KV: this split's partial state (unnormalised O, running max in log2
+        // units, L) is written through to the device-coherent level (sc1 stores: the
+        // workgroup that combines may run on another XCD), then counted in for this
+        // (query block, head).  The workgroup that counts last combines every split
+        // in split order -- M = max_s m_s, out = Σ_s O_s 2^(m_s - M) / Σ_s L_s 2^(m_s - M)
+        // -- and re-arms the counter for the next call.  No workgroup waits for
+        // another.
+        constexpr int kSc1 = 16;    // cache policy: sc1
+        const int item = head * gridDim.x + blockIdx.x;
+        // this query block's 64 rows of split s: O [64][HD] and (m, L) [64]
+        auto o_rsrc = [&](int s) {
+            return __builtin_amdgcn_make_buffer_rsrc(opart + (((size_t)s * gridDim.y + head) * n_q + q0) * HD, 0,
+                                                     QROWS * HD * 4, kRsrcW3);
+        };
+        auto ml_rsrc = [&](int s) {
+            return __builtin_amdgcn_make_buffer_rsrc(mlpart + ((size_t)s * gridDim.y + head) * n_q + q0, 0,
+                                                     QROWS * 8, kRsrcW3);
+        };
+        const int ooff = ((16 * w + qi) * HD + 4 * G) * 4;   // this lane's first 16 bytes in a block
+        const int moff = (16 * w + qi) * 8;
+        {
+            const __amdgpu_buffer_rsrc_t rs = o_rsrc(split);
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-            *reinterpret_cast<float4*>(orow + 16 * dt) = make_float4(O[dt][0], O[dt][1], O[dt][2], O[dt][3]);
-        if (G == 0) mlpart[prow] = make_float2(rref, L);
-    }
-}
-
-// Combine of the KV splits of one (head, query row): with M the largest running
-// max, out = Σ_s O_s 2^(m_s - M) / Σ_s L_s 2^(m_s - M), splits in order.
-// grid (n_q / 8, H), block 256 (one thread per dim); each thread combines 8
-// query rows side by side, so its loads of a split are independent.
-constexpr int kCombRows = 8;
-__global__ __launch_bounds__(256) void fa_combine_k(float* __restrict__ out, const float* __restrict__ opart,
-                                                   const float2* __restrict__ mlpart, int n_q, int nsplit) {
-    const int row0 = blockIdx.x * kCombRows, head = blockIdx.y, d = threadIdx.x;
-    const int H = gridDim.y;
-    float M[kCombRows], o[kCombRows], l[kCombRows];
+            for (int dt = 0; dt < 16; dt++)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v4u{__float_as_uint(O[dt][0]), __float_as_uint(O[dt][1]), __float_as_uint(O[dt][2]),
+                        __float_as_uint(O[dt][3])},
+                    rs, ooff + dt * 64, 0, kSc1);
+            if (G == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(v2u{__float_as_uint(rref), __float_as_uint(L)}, ml_rsrc(split),
+                                                      moff, 0, kSc1);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            s_last = __hip_atomic_fetch_add(cnt + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+        __syncthreads();
+        if (s_last) {
+            auto ml_of = [&](int s) -> float2 {
+                const v2u v = __builtin_amdgcn_raw_buffer_load_b64(ml_rsrc(s), moff, 0, kSc1);
+                return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
+            };
+            float Mx = -__builtin_inff();
+            for (int s = 0; s < nsplit; s++) Mx = fmaxf(Mx, ml_of(s).x);
+            float o[16][4];
 #pragma unroll
-    for (int r = 0; r < kCombRows; r++) {
-        M[r] = -__builtin_inff();
-        o[r] = 0.f;
-        l[r] = 0.f;
-    }
-    for (int s = 0; s < nsplit; s++)
+            for (int dt = 0; dt < 16; dt++)
 #pragma unroll
-        for (int r = 0; r < kCombRows; r++) M[r] = fmaxf(M[r], mlpart[((size_t)s * H + head) * n_q + row0 + r].x);
-    for (int s = 0; s < nsplit; s++) {
+                for (int r = 0; r < 4; r++) o[dt][r] = 0.f;
+            float l = 0.f;
+            for (int s = 0; s < nsplit; s++) {
+                const float2 ml = ml_of(s);
+                const float a = exp2f(ml.x - Mx);
+                if (s == split) {      // this workgroup's own split, still in registers
 #pragma unroll
-        for (int r = 0; r < kCombRows; r++) {
-            const size_t prow = ((size_t)s * H + head) * n_q + row0 + r;
-            const float2 ml = mlpart[prow];
-            const float a = exp2f(ml.x - M[r]);
-            o[r] = fmaf(a, opart[prow * HD + d], o[r]);
-            l[r] = fmaf(a, ml.y, l[r]);
+                    for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) o[dt][r] = fmaf(a, O[dt][r], o[dt][r]);
+                } else {
+                    const __amdgpu_buffer_rsrc_t rs = o_rsrc(s);
+#pragma unroll
+                    for (int dt = 0; dt < 16; dt++) {
+                        const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs, ooff + dt * 64, 0, kSc1);
+                        o[dt][0] = fmaf(a, __uint_as_float(v.x), o[dt][0]);
+                        o[dt][1] = fmaf(a, __uint_as_float(v.y), o[dt][1]);
+                        o[dt][2] = fmaf(a, __uint_as_float(v.z), o[dt][2]);
+                        o[dt][3] = fmaf(a, __uint_as_float(v.w), o[dt][3]);
+                    }
+                }
+                l = fmaf(a, ml.y, l);
+            }
+            float* orow = out + (size_t)qrow * HD + 4 * G;
+#pragma unroll
+            for (int dt = 0; dt < 16; dt++)
+                *reinterpret_cast<float4*>(orow + 16 * dt) =
+                    make_float4(l > 0.f ? o[dt][0] / l : 0.f, l > 0.f ? o[dt][1] / l : 0.f,
+                                l > 0.f ? o[dt][2] / l : 0.f, l > 0.f ? o[dt][3] / l : 0.f);
+            if (tid == 0) __hip_atomic_store(cnt + item, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-#pragma unroll
-    for (int r = 0; r < kCombRows; r++)
-        out[((size_t)head * n_q + row0 + r) * HD + d] = l[r] > 0.f ? o[r] / l[r] : 0.f;
 }
 
 // -------------------------------------------------------------- launchers --
@@ -725,16 +765,17 @@ size_t fa_part_bytes(int n_q, int n_heads, int nsplit) {
     return nsplit > 1 ? (size_t)nsplit * n_heads * n_q * (HD + 2) * sizeof(float) : 0;
 }
 
+size_t fa_cnt_bytes(int n_q, int n_heads, int nsplit) {
+    return nsplit > 1 ? (size_t)(n_q / QROWS) * n_heads * sizeof(int) : 0;
+}
+
 hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                           const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
-                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, hipStream_t st) {
+                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, hipStream_t st) {
     float* opart = part;
     float2* mlpart = part ? reinterpret_cast<float2*>(part + (size_t)nsplit * n_heads * n_q * HD) : nullptr;
     hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads, nsplit), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc,
-                       out, n_q, n_kv, off, n_tile, ratio, kv_cap, nsplit, opart, mlpart);
-    if (nsplit > 1)
-        hipLaunchKernelGGL(fa_combine_k, dim3(n_q / kCombRows, n_heads), dim3(256), 0, st, out, opart, mlpart, n_q,
-                           nsplit);   // n_q is a multiple of 64
+                       out, n_q, n_kv, off, n_tile, ratio, kv_cap, nsplit, opart, mlpart, cnt);
     return hipGetLastError();
 }
 

@@ -34,7 +34,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // the retired buffers of a slot add up to at most twice its final size.  Not
 // safe for concurrent calls from several threads (the reference's scratch has
 // the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlots = 8 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlotAttnCnt = 8, kSlots = 9 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -668,12 +668,15 @@ int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, 
     // workspace falls back to one split (no workspace; same algorithm, the fp32
     // sums of O and L in one order instead of a combine of partial ranges).
     if (nsplit > 1 && kv_splits == 0 && capturing(st) &&
-        !scratch_has(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit)))
+        !(scratch_has(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit)) &&
+          scratch_has(kSlotAttnCnt, rt4::fa_cnt_bytes(n_q, n_heads, nsplit))))
         nsplit = 1;
-    void* part = nullptr;
-    if (nsplit > 1 && (rc = lib_scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st))) return rc;
+    void *part = nullptr, *cnt = nullptr;
+    if (nsplit > 1 && ((rc = lib_scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st)) ||
+                       (rc = lib_scratch(kSlotAttnCnt, rt4::fa_cnt_bytes(n_q, n_heads, nsplit), &cnt, st, true))))
+        return rc;
     return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
-                                          kv_cap, nsplit, static_cast<float*>(part), st),
+                                          kv_cap, nsplit, static_cast<float*>(part), static_cast<int*>(cnt), st),
                       "k_attention launch");
 }
 

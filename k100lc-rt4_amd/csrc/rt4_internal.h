@@ -92,11 +92,14 @@ hipError_t launch_kv_append_k(uint32_t* kc, float* ksc, const float* kf, int t0,
 hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int t0, int T, int H,
                               int D, int BG, int kv_total, hipStream_t st);
 // KV splits per (query block, head) that balance the grid over `cus` CUs, and
-// the workspace they need (0 for one split).
+// the workspace they need (0 for one split): partial states, and one counter per
+// (query block, head) that must be zero before the first launch (every launch
+// leaves them zero again).
 int fa_splits(int n_q, int n_heads, int n_tile, int cus);
 size_t fa_part_bytes(int n_q, int n_heads, int nsplit);
+size_t fa_cnt_bytes(int n_q, int n_heads, int nsplit);
 hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                           const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
-                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, hipStream_t st);
+                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, hipStream_t st);
 
 }  // namespace rt4
