@@ -26,7 +26,11 @@
  *                          = bits 4e..4e+3, two's complement, low nibble first.
  *   ws   uint16 [N][K/128] fp16 bit patterns of the per-128-group weight scales,
  *                          row-major (the reference passes these as `const float*`).
- *   wsc_gm float [K/128][N] fp32 group-major weight scales (src/model.cpp:190-202).
+ *   wsc_gm float [K/128][N] fp32 group-major weight scales (src/model.cpp:190-202):
+ *                          the fp16 scales of ws widened to fp32, as
+ *                          rt4_make_group_major writes them.  The prefill GEMMs
+ *                          use them as such (11 significant bits); other fp32
+ *                          values would count to 16 significant bits.
  *   xq   int8  [rows][K]   activation codes in "interleaved" order: for each
  *                          8-element block b, bytes [a(8b+0) a(8b+2) a(8b+4) a(8b+6)
  *                          a(8b+1) a(8b+3) a(8b+5) a(8b+7)].  Internal to this
@@ -174,7 +178,9 @@ int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, 
 
 /* The same GEMM on int8 codes: xq int8 [M][K] interleaved (rt4_quant_rows_i8
  * output), sc f32 [K/128][M].  No reference counterpart (it is k_gemm_i4_a8
- * without the digit planes).  M >= 1, N >= 1, K % 128 == 0. */
+ * without the digit planes).  M >= 1, N >= 1, K % 128 == 0.  Each group's scale
+ * product sc*wsc_gm is formed to within a few units in the last place of fp32 (the
+ * reference rounds it once); an infinite sc gives NaN outputs in its row. */
 int rt4_gemm_w4a8_i8(float* c, const uint32_t* wq, const float* wsc_gm, const int8_t* xq,
                      const float* sc, int M, int N, int K, void* stream);
 

@@ -22,10 +22,14 @@
 //     facc += f32(acc) * S,   S = sa * sb,   acc = 16*I exactly (x16 nibble unpack),
 // and the result is scaled by 1/16 once at the end (a power of two, so the bits
 // equal those of scaling every term).  S is formed on the matrix core: one
-// v_mfma_f32_32x32x2_f32 per row tile (its k = 1 half zero) gives the rank-1
-// products sa (x) sb in the accumulator layout, each a single fp32 product
-// rounded once.  (The two-block form, one MFMA per pair of row tiles, needs 16
-// more registers live, which this loop does not have.)
+// v_mfma_f32_32x32x8_bf16 per row tile gives the rank-1 products sa (x) sb in
+// the accumulator layout.  Its operands are exact bf16 splits: sa = b1 + b2 + b3
+// (three bf16 values, made once per call by split_scales_k: 3 x 8 significant
+// bits hold fp32's 24) and sb = c1 + c2 (RT4 weight scales are fp16 values, 11
+// significant bits), so the six products b_i * c_j are exact and the MFMA's
+// fp32 sum of them is sa * sb to within a few units in the last place.  The
+// bf16 MFMA occupies the matrix core ~15 cycles against ~70 for the fp32 one
+// (v_mfma_f32_32x32x2_f32 with its k = 1 half zero), measured.
 //
 // What bounds this kernel on gfx950 is instruction issue: measured, a SIMD with
 // two such waves issues about one instruction per 4 cycles whatever its kind
@@ -38,11 +42,15 @@
 // base pointers advanced by a constant per unit; tile bookkeeping is a few
 // scalar counters.  The MFMAs of a row tile are interleaved one by one with the
 // fold of the previous row tile (and with the unpack of the next k-step), in an
-// order the compiler may not change (sched_barrier), so the matrix core and the
-// vector ALU work at the same time and no fold waits for the MFMA just issued.
+// order the compiler may not change (sched_barrier; every folded value also
+// passes through an empty asm statement where it is formed, without which the
+// compiler sinks three of the four folds of a unit past the barrier into one
+// block and spills), so the matrix core and the vector ALU work at the same
+// time and no fold waits for the MFMA just issued.
 //
 // Data movement.  Per unit the workgroup moves 16 KB of int8 activations, 16 KB
-// of packed weights and the two scale vectors from global memory straight into
+// of packed weights and the two scale vectors (the activation scales as their
+// 16-byte bf16 splits) from global memory straight into
 // LDS with global_load_lds_dwordx4 (no VGPR round trip), four stages deep (the
 // unit three ahead is loading while a unit computes).  Each wave loads exactly
 // the weight rows it reads; the activation tile is shared by all waves (one
@@ -66,6 +74,17 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v4h __attribute__((ext_vector_type(4)));   // four bf16 bit patterns (MFMA operand)
+
+// sb = c1 + c2 with c1 its bf16 truncation and c2 the exact rest (an fp16 value has
+// 11 significant bits, so the rest has at most 3), as the B operand of the scale
+// MFMA: (c1, c2, c1, c2) in lanes 0..31, (c1, c2, 0, 0) in lanes 32..63.
+__device__ __forceinline__ v4h split_sb(float sb, int lh) {
+    const uint32_t c1 = __float_as_uint(sb) & 0xFFFF0000u;
+    const uint32_t c2 = __float_as_uint(sb - __uint_as_float(c1));
+    const uint32_t pk = __builtin_amdgcn_perm(c2, c1, 0x07060302u);   // c1 in the low half, c2 high
+    return __builtin_bit_cast(v4h, make_uint2(pk, lh ? 0u : pk));
+}
 
 constexpr int BM = 128;           // activation rows per tile
 constexpr int BN = 256;           // weight rows (output columns) per tile
@@ -73,7 +92,7 @@ constexpr int NT = 512;           // 8 waves
 constexpr int NS = 4;             // LDS stages
 constexpr int A_ST = BM * 128;    // int8 activation tile per stage
 constexpr int B_ST = BN * 64;     // packed weight tile per stage
-constexpr int S_ST = 2048;        // sa (512 B) + sb (1024 B) + 512 B written by the two idle waves
+constexpr int S_ST = 3584;        // sa splits (2048 B) + sb (1024 B) + 512 B written by the two idle waves
 constexpr int LDS_B = 0;                       // weight stages
 constexpr int LDS_A = LDS_B + NS * B_ST;       // activation stages
 constexpr int LDS_S = LDS_A + NS * A_ST;       // scale stages
@@ -156,8 +175,9 @@ __device__ __forceinline__ void add4_dev16(v16i& f, const float* p) {
 //      wave w loads rows 16w..16w+15 (two instructions of 8 rows x 128 B)
 //   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3);
 //      wave w loads rows 32w..32w+31, the ones it reads
-//   S  sa[128] f32 (waves 0, 1), sb[256] f32 (waves 2..5); waves 6, 7 repeat an sb
-//      load into the spare 512 B so that every wave issues the same count.
+//   S  sa splits [128 rows][16 B] (waves 0, 1: one 16-byte load per lane), sb[256]
+//      f32 (waves 2..5); waves 6, 7 repeat an sb load into the spare 512 B so that
+//      every wave issues the same count.
 struct DmaOff {
     uint32_t a[2], b[2], s;
 };
@@ -178,7 +198,7 @@ __device__ __forceinline__ DmaOff dma_offsets(int bm, int bn, int M, int N, int 
         o.b[t] = (uint32_t)gr * (uint32_t)(K >> 1) + c * 16;
     }
     if (w < 2)
-        o.s = (uint32_t)min(bm + 64 * w + lane, M - 1) * 4u;
+        o.s = (uint32_t)min(bm + 64 * w + lane, M - 1) * 16u;
     else
         o.s = (uint32_t)min(bn + 64 * ((w - 2) & 3) + lane, N - 1) * 4u;
     return o;
@@ -197,7 +217,7 @@ struct TileRef {
 template <bool GSUM>
 __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ A,
                                                      const uint32_t* __restrict__ W,
-                                                     const float* __restrict__ sa,
+                                                     const uint4* __restrict__ sa,
                                                      const float* __restrict__ sb,
                                                      float* __restrict__ C,
                                                      int32_t* __restrict__ gsum,
@@ -226,11 +246,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const int r = 32 * w + lr;
         rb[s2] = LDS_B + r * 64 + (((2 * s2 + lh) ^ ((r >> 2) & 3)) * 16);
     }
-    int rsa = LDS_S + lr * 4, rsb = LDS_S + 512 + (32 * w + lr) * 4;
+    int rsa = LDS_S + lr * 16 + lh * 8, rsb = LDS_S + 2048 + (32 * w + lr) * 4;
     // per-wave LDS destinations of the DMA (m0 = base + stage immediate)
     const uint32_t L = lds_addr(lds);
     const uint32_t dstA = L + LDS_A + 2 * w * 1024, dstB = L + LDS_B + 2 * w * 1024;
-    const uint32_t dstS = L + LDS_S + (w < 2 ? w * 256 : w < 6 ? 512 + (w - 2) * 256 : 1536);
+    const uint32_t dstS = L + LDS_S + (w < 2 ? w * 1024 : w < 6 ? 2048 + (w - 2) * 256 : 3072);
 
     // facc[ii]: row tile ii (rows 32 ii..32 ii+31) x this wave's 32 columns; lane (lr, lh)
     // holds column 32w + lr, rows 32 ii + 8q + 4lh + e in register 4q + e.
@@ -247,24 +267,27 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const uint32_t x0 = (ks & 1) ? p.z : p.x, x1 = (ks & 1) ? p.w : p.y;
         bu_[ks] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
     };
-    // Scale products of row tile ii on the matrix core: v_mfma_f32_32x32x2_f32 with
-    // A = [sa | 0] and B = [sb ; 0] (lanes 32..63 supply k = 1) gives
-    // S[r] = sa[row of register r] * sb[this lane's column] in the accumulator
-    // layout of the int8 tiles, each a single fp32 product rounded once (the bits of
-    // sa * sb on the vector ALU; the zero half adds +0 exactly).  One of the three
-    // fold operations per output thus leaves the vector ALU.
-    auto sa_of = [&](int ii) __attribute__((always_inline)) -> float {
-        const float a = *reinterpret_cast<const float*>(lds + rsa + ii * 128);
-        return lh ? 0.f : a;
+    // Scale products of row tile ii on the matrix core: v_mfma_f32_32x32x8_bf16 (lane
+    // l supplies row / column l & 31 at k = 4(l >> 5) .. +3) with
+    //   A: lanes 0..31 (b1, b1, b2, b2), lanes 32..63 (b3, b3, 0, 0)  of sa's split,
+    //   B: lanes 0..31 (c1, c2, c1, c2), lanes 32..63 (c1, c2, 0, 0)  of sb's split,
+    // gives S[r] = sum_ij b_i c_j = sa[row of register r] * sb[this lane's column] in
+    // the accumulator layout of the int8 tiles.  A row's split record holds the two
+    // dword pairs in that order, so lane (lr, lh) reads its pair at 8 * lh.
+    auto sa_of = [&](int ii) __attribute__((always_inline)) -> v4h {
+        return *reinterpret_cast<const v4h*>(lds + rsa + ii * 512);
     };
-    auto scales = [&](float saz, float sbz) __attribute__((always_inline)) -> v16f {
-        return __builtin_amdgcn_mfma_f32_32x32x2f32(saz, sbz, zero16f, 0, 0, 0);
+    auto scales = [&](v4h sa_split, v4h sb_split) __attribute__((always_inline)) -> v16f {
+        return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sa_split, sb_split, zero16f, 0, 0, 0);
     };
     // quarter q of the fold of row tile ii (registers 4q..4q+3)
     auto fold_q = [&](v16i& fa, const v16i& acc, const v16f& S, int ii, int q, const TileRef& x) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 4 * q; r < 4 * q + 4; r++)
-            fa[r] = __float_as_int(fmaf((float)acc[r], S[r], __int_as_float(fa[r])));
+        for (int r = 4 * q; r < 4 * q + 4; r++) {
+            int v = __float_as_int(fmaf((float)acc[r], S[r], __int_as_float(fa[r])));
+            asm volatile("" : "+v"(v));   // formed here, not sunk past the next MFMAs
+            fa[r] = v;
+        }
         if (GSUM && x.g >= 0) {
             const int nn = x.bn + 32 * w + lr;
 #pragma unroll
@@ -382,7 +405,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         dtm = t0 - dtn * ntm;
     }
     const void* sbase = (w < 2 ? (const void*)sa : (const void*)sb);
-    const uint32_t s_step = (w < 2 ? (uint32_t)M : (uint32_t)N) * 4u;
+    const uint32_t s_step = w < 2 ? (uint32_t)M * 16u : (uint32_t)N * 4u;
     DmaOff off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
     off.a[0] += dg0 * 128;
     off.a[1] += dg0 * 128;
@@ -396,7 +419,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         dma16<1024>(off.a[1], A, da);
         dma16<0>(off.b[0], W, db);
         dma16<1024>(off.b[1], W, db);
-        dma4<0>(off.s, sbase, ds);
+        if (w < 2) dma16<0>(off.s, sbase, ds);
+        else dma4<0>(off.s, sbase, ds);
     };
     auto advance_dma = [&]() __attribute__((always_inline)) {
         if (--dleft == 0) {
@@ -496,8 +520,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // row tile 0, with the unpack of this unit's weights and the fold of the
         // previous unit's last tile
         read_a(a_nxt, 1);
-        float sbz = *reinterpret_cast<const float*>(lds + rsb);
-        sbz = lh ? 0.f : sbz;
+        const v4h sbz = split_sb(*reinterpret_cast<const float*>(lds + rsb), lh);
         // (for the first unit of a segment accB is zero: the fold adds exact zeros)
         step(a_cur, accA, accB, facc[3], 3, xprev, true, true);
         S = scales(sa_of(0), sbz);
@@ -509,7 +532,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         read_a(a_nxt, 3);
         step(a_cur, accA, accB, facc[1], 1, x, false, true);
         S = scales(sa_of(2), sbz);
-        const float sa3 = sa_of(3);   // read before the barrier: the stage is refilled after it
+        const v4h sa3 = sa_of(3);   // read before the barrier: the stage is refilled after it
         // row tile 3.  The DMA of unit i+1 has landed once at most the two younger
         // units' loads are pending (three units in flight), and every wave has issued
         // its last read of this stage (the barrier waits for LDS reads).  Near the
@@ -577,7 +600,7 @@ GemmPlan gemm_plan(int M, int N, int K, int cus) {
 }
 
 hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint32_t* W,
-                            const float* sa, const float* sb, int M, int N, int K, const GemmPlan& p,
+                            const uint4* sa, const float* sb, int M, int N, int K, const GemmPlan& p,
                             float* part, int* cnt, hipStream_t st) {
     if (gsum)
         hipLaunchKernelGGL(gemm_w4a8_k<true>, dim3(p.P), dim3(NT), 0, st, A, W, sa, sb, C, gsum, part, cnt, M, N,
@@ -585,6 +608,19 @@ hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint
     else
         hipLaunchKernelGGL(gemm_w4a8_k<false>, dim3(p.P), dim3(NT), 0, st, A, W, sa, sb, C, gsum, part, cnt, M,
                            N, K, p.ntm, p.T);
+    return hipGetLastError();
+}
+
+// The activation scales' bf16 splits (split_scale_bf16x3) for the scale MFMA.
+__global__ __launch_bounds__(256) void split_scales_k(const float* __restrict__ s, uint4* __restrict__ out,
+                                                      size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = split_scale_bf16x3(s[i]);
+}
+
+hipError_t launch_split_scales(uint4* out, const float* s, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(split_scales_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, out, n);
     return hipGetLastError();
 }
 
