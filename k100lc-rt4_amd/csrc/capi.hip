@@ -34,7 +34,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // the retired buffers of a slot add up to at most twice its final size.  Not
 // safe for concurrent calls from several threads (the reference's scratch has
 // the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlotAttnCnt = 8, kSlotGemmSc = 9, kSlots = 10 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlotAttnCnt = 8, kSlots = 9 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -139,35 +139,17 @@ int device_cus(int* cus) {
     return RT4_OK;
 }
 
-// Library scratch for the bf16 splits of the M x K/128 activation scales the GEMM's
-// scale products take (launch_split_scales).
-int gemm_scale_split(int M, int K, uint4** out, hipStream_t st) {
-    void* p = nullptr;
-    const int rc = lib_scratch(kSlotGemmSc, (size_t)M * (K / 128) * sizeof(uint4), &p, st);
-    *out = static_cast<uint4*>(p);
-    return rc;
-}
-
-// The GEMM launch with its library-owned split-tile workspace.  sc_split: the
-// activation scales' bf16 splits when the caller's launch already wrote them
-// (the digit recombination does), else null and they are made here from sc.
+// The GEMM launch with its library-owned split-tile workspace.
 int run_gemm(const char* who, int32_t* gsum, float* c, const uint32_t* wq, const float* wsc_gm,
-             const int8_t* xq, const float* sc, const uint4* sc_split, int M, int N, int K, hipStream_t st) {
+             const int8_t* xq, const float* sc, int M, int N, int K, hipStream_t st) {
     int cus = 0, rc = device_cus(&cus);
     if (rc) return rc;
     const rt4::GemmPlan plan = rt4::gemm_plan(M, N, K, cus);
     void *part = nullptr, *cnt = nullptr;
     if ((rc = lib_scratch(kSlotGemmPart, plan.part_bytes, &part, st))) return rc;
     if ((rc = lib_scratch(kSlotGemmCnt, plan.cnt_bytes, &cnt, st, true))) return rc;
-    if (!sc_split) {
-        uint4* sp = nullptr;
-        if ((rc = gemm_scale_split(M, K, &sp, st))) return rc;
-        hipError_t e = rt4::launch_split_scales(sp, sc, (size_t)M * (K / 128), st);
-        if (e != hipSuccess) return hip_status(e, who);
-        sc_split = sp;
-    }
-    return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc_split, wsc_gm, M, N, K, plan,
-                                            static_cast<float*>(part), static_cast<int*>(cnt), st),
+    return hip_status(rt4::launch_gemm_w4a8(c, gsum, xq, wq, sc, wsc_gm, M, N, K, plan, static_cast<float*>(part),
+                                            static_cast<int*>(cnt), st),
                       who);
 }
 
@@ -305,7 +287,7 @@ int gemm_i8_common(const char* who, int32_t* gsum, float* c, const uint32_t* wq,
     if (rc) return rc;
     if (!aligned(wq, 16) || !aligned(xq, 16) || !aligned(c, 4) || !aligned(sc, 4) || !aligned(wsc_gm, 4))
         return fail(RT4_E_ARG, "%s: misaligned pointer (wq and xq need 16 bytes, ws 4)", who);
-    return run_gemm(who, gsum, c, wq, wsc_gm, xq, sc, nullptr, M, N, K, as_stream(stream));
+    return run_gemm(who, gsum, c, wq, wsc_gm, xq, sc, M, N, K, as_stream(stream));
 }
 
 }  // namespace
@@ -577,12 +559,10 @@ int rt4_gemm_w4a4(float* c, const uint32_t* wq, const float* wsc_gm, const uint3
     // buffer for them).
     hipStream_t st = as_stream(stream);
     void* q = nullptr;
-    uint4* sp = nullptr;
-    if ((rc = lib_scratch(kSlotGemmA, (size_t)M * K, &q, st)) || (rc = gemm_scale_split(M, K, &sp, st))) return rc;
-    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), nullptr, aq, M, K, st, asc_gm, sp);
+    if ((rc = lib_scratch(kSlotGemmA, (size_t)M * K, &q, st))) return rc;
+    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), nullptr, aq, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4 code expansion");
-    return run_gemm("k_gemm_i4 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), asc_gm, sp, M, N, K,
-                    st);
+    return run_gemm("k_gemm_i4 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), asc_gm, M, N, K, st);
 }
 
 
@@ -616,12 +596,9 @@ int rt4_gemm_w4a8(float* c, float* c2, const uint32_t* wq, const float* wsc_gm, 
     hipStream_t st = as_stream(stream);
     void* q = c2;
     if ((size_t)M * N * sizeof(float) < need && (rc = lib_scratch(kSlotGemmA, need, &q, st))) return rc;
-    uint4* sp = nullptr;
-    if ((rc = gemm_scale_split(M, K, &sp, st))) return rc;
-    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st, sc, sp);
+    hipError_t e = rt4::launch_hl_to_i8(static_cast<int8_t*>(q), ah, al, M, K, st);
     if (e != hipSuccess) return hip_status(e, "k_gemm_i4_a8 digit recombination");
-    return run_gemm("k_gemm_i4_a8 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), sc, sp, M, N, K,
-                    st);
+    return run_gemm("k_gemm_i4_a8 launch", nullptr, c, wq, wsc_gm, static_cast<const int8_t*>(q), sc, M, N, K, st);
 }
 
 int rt4_make_group_major(float* wsc_gm, const uint16_t* ws, int N, int K, void* stream) {

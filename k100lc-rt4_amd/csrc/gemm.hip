@@ -24,8 +24,9 @@
 // equal those of scaling every term).  S is formed on the matrix core: one
 // v_mfma_f32_32x32x8_bf16 per row tile gives the rank-1 products sa (x) sb in
 // the accumulator layout.  Its operands are exact bf16 splits: sa = b1 + b2 + b3
-// (three bf16 values, made once per call by split_scales_k: 3 x 8 significant
-// bits hold fp32's 24) and sb = c1 + c2 (RT4 weight scales are fp16 values, 11
+// (three bf16 values, 3 x 8 significant bits holding fp32's 24, made per unit by
+// the two waves that load sa, one row per lane, into LDS before the unit's
+// barrier) and sb = c1 + c2 (RT4 weight scales are fp16 values, 11
 // significant bits), so the six products b_i * c_j are exact and the MFMA's
 // fp32 sum of them is sa * sb to within a few units in the last place.  The
 // bf16 MFMA occupies the matrix core ~15 cycles against ~70 for the fp32 one
@@ -49,8 +50,7 @@
 // time and no fold waits for the MFMA just issued.
 //
 // Data movement.  Per unit the workgroup moves 16 KB of int8 activations, 16 KB
-// of packed weights and the two scale vectors (the activation scales as their
-// 16-byte bf16 splits) from global memory straight into
+// of packed weights and the two scale vectors from global memory straight into
 // LDS with global_load_lds_dwordx4 (no VGPR round trip), four stages deep (the
 // unit three ahead is loading while a unit computes).  Each wave loads exactly
 // the weight rows it reads; the activation tile is shared by all waves (one
@@ -92,7 +92,8 @@ constexpr int NT = 512;           // 8 waves
 constexpr int NS = 4;             // LDS stages
 constexpr int A_ST = BM * 128;    // int8 activation tile per stage
 constexpr int B_ST = BN * 64;     // packed weight tile per stage
-constexpr int S_ST = 3584;        // sa splits (2048 B) + sb (1024 B) + 512 B written by the two idle waves
+constexpr int S_ST = 4096;        // sa (512 B) + sb (1024 B) + 512 B written by the two idle waves + sa splits (2048 B)
+constexpr int S_SPLIT = 2048;     // offset of the sa splits in a scale stage
 constexpr int LDS_B = 0;                       // weight stages
 constexpr int LDS_A = LDS_B + NS * B_ST;       // activation stages
 constexpr int LDS_S = LDS_A + NS * A_ST;       // scale stages
@@ -175,9 +176,9 @@ __device__ __forceinline__ void add4_dev16(v16i& f, const float* p) {
 //      wave w loads rows 16w..16w+15 (two instructions of 8 rows x 128 B)
 //   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3);
 //      wave w loads rows 32w..32w+31, the ones it reads
-//   S  sa splits [128 rows][16 B] (waves 0, 1: one 16-byte load per lane), sb[256]
-//      f32 (waves 2..5); waves 6, 7 repeat an sb load into the spare 512 B so that
-//      every wave issues the same count.
+//   S  sa[128] f32 (waves 0, 1), sb[256] f32 (waves 2..5); waves 6, 7 repeat an sb
+//      load into the spare 512 B so that every wave issues the same count; then
+//      the bf16 splits of sa, [128 rows][16 B] at S_SPLIT, written by waves 0, 1.
 struct DmaOff {
     uint32_t a[2], b[2], s;
 };
@@ -198,7 +199,7 @@ __device__ __forceinline__ DmaOff dma_offsets(int bm, int bn, int M, int N, int 
         o.b[t] = (uint32_t)gr * (uint32_t)(K >> 1) + c * 16;
     }
     if (w < 2)
-        o.s = (uint32_t)min(bm + 64 * w + lane, M - 1) * 16u;
+        o.s = (uint32_t)min(bm + 64 * w + lane, M - 1) * 4u;
     else
         o.s = (uint32_t)min(bn + 64 * ((w - 2) & 3) + lane, N - 1) * 4u;
     return o;
@@ -217,7 +218,7 @@ struct TileRef {
 template <bool GSUM>
 __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ A,
                                                      const uint32_t* __restrict__ W,
-                                                     const uint4* __restrict__ sa,
+                                                     const float* __restrict__ sa,
                                                      const float* __restrict__ sb,
                                                      float* __restrict__ C,
                                                      int32_t* __restrict__ gsum,
@@ -246,11 +247,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const int r = 32 * w + lr;
         rb[s2] = LDS_B + r * 64 + (((2 * s2 + lh) ^ ((r >> 2) & 3)) * 16);
     }
-    int rsa = LDS_S + lr * 16 + lh * 8, rsb = LDS_S + 2048 + (32 * w + lr) * 4;
+    int rsa = LDS_S + S_SPLIT + lr * 16 + lh * 8, rsb = LDS_S + 512 + (32 * w + lr) * 4;
     // per-wave LDS destinations of the DMA (m0 = base + stage immediate)
     const uint32_t L = lds_addr(lds);
     const uint32_t dstA = L + LDS_A + 2 * w * 1024, dstB = L + LDS_B + 2 * w * 1024;
-    const uint32_t dstS = L + LDS_S + (w < 2 ? w * 1024 : w < 6 ? 2048 + (w - 2) * 256 : 3072);
+    const uint32_t dstS = L + LDS_S + (w < 2 ? w * 256 : w < 6 ? 512 + (w - 2) * 256 : 1536);
 
     // facc[ii]: row tile ii (rows 32 ii..32 ii+31) x this wave's 32 columns; lane (lr, lh)
     // holds column 32w + lr, rows 32 ii + 8q + 4lh + e in register 4q + e.
@@ -405,7 +406,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         dtm = t0 - dtn * ntm;
     }
     const void* sbase = (w < 2 ? (const void*)sa : (const void*)sb);
-    const uint32_t s_step = w < 2 ? (uint32_t)M * 16u : (uint32_t)N * 4u;
+    const uint32_t s_step = (w < 2 ? (uint32_t)M : (uint32_t)N) * 4u;
     DmaOff off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
     off.a[0] += dg0 * 128;
     off.a[1] += dg0 * 128;
@@ -419,8 +420,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         dma16<1024>(off.a[1], A, da);
         dma16<0>(off.b[0], W, db);
         dma16<1024>(off.b[1], W, db);
-        if (w < 2) dma16<0>(off.s, sbase, ds);
-        else dma4<0>(off.s, sbase, ds);
+        dma4<0>(off.s, sbase, ds);
     };
     auto advance_dma = [&]() __attribute__((always_inline)) {
         if (--dleft == 0) {
@@ -450,6 +450,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         cur.bn = tn * BN;
     }
 
+    // The bf16 splits of a stage's activation scales (split_scale_bf16x3), one row
+    // per lane of waves 0 and 1, which load those scales: called after their wait
+    // for that stage's DMA and before the barrier that orders these LDS writes
+    // before every wave's reads.
+    auto split_stage = [&](int stn) __attribute__((always_inline)) {
+        if (w < 2) {
+            unsigned char* b = lds + LDS_S + stn * S_ST;
+            const float sv = *reinterpret_cast<const float*>(b + (64 * w + lane) * 4);
+            *reinterpret_cast<uint4*>(b + S_SPLIT + (64 * w + lane) * 16) = split_scale_bf16x3(sv);
+        }
+    };
+
     // prologue: DMA of units 0..3, then the fragments of unit 0
     issue(0);
     if (n > 1) { advance_dma(); issue(1); }
@@ -457,6 +469,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     if (n > 3) { advance_dma(); issue(3); }
     if (n > 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * DMA_PER_UNIT) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    split_stage(0);
     __syncthreads();
     v4i a_cur[4], a_nxt[4], bu[4];
     uint4 bp[2];
@@ -542,6 +555,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // variant stores as it goes.  In those cases no count bound is safe: drain.
         if (GSUM || first || i + 3 >= n) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
+        split_stage((st + 1) & (NS - 1));   // unit i+1's scales (stale past the share's end: unread)
         __syncthreads();
         if (i + 4 < n) {
             advance_dma();
@@ -600,7 +614,7 @@ GemmPlan gemm_plan(int M, int N, int K, int cus) {
 }
 
 hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint32_t* W,
-                            const uint4* sa, const float* sb, int M, int N, int K, const GemmPlan& p,
+                            const float* sa, const float* sb, int M, int N, int K, const GemmPlan& p,
                             float* part, int* cnt, hipStream_t st) {
     if (gsum)
         hipLaunchKernelGGL(gemm_w4a8_k<true>, dim3(p.P), dim3(NT), 0, st, A, W, sa, sb, C, gsum, part, cnt, M, N,
@@ -608,19 +622,6 @@ hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint
     else
         hipLaunchKernelGGL(gemm_w4a8_k<false>, dim3(p.P), dim3(NT), 0, st, A, W, sa, sb, C, gsum, part, cnt, M,
                            N, K, p.ntm, p.T);
-    return hipGetLastError();
-}
-
-// The activation scales' bf16 splits (split_scale_bf16x3) for the scale MFMA.
-__global__ __launch_bounds__(256) void split_scales_k(const float* __restrict__ s, uint4* __restrict__ out,
-                                                      size_t n) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) out[i] = split_scale_bf16x3(s[i]);
-}
-
-hipError_t launch_split_scales(uint4* out, const float* s, size_t n, hipStream_t st) {
-    if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(split_scales_k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, s, out, n);
     return hipGetLastError();
 }
 

@@ -219,9 +219,7 @@ hipError_t launch_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows
 // h/l digit planes -> int8 codes q8 = 16h + l, interleaved, for the MFMA GEMM.
 // Bytewise: x = (h<<4) | (l^8) is q8+8 with no carries between bytes; the
 // per-byte subtraction of 8 then uses the borrow-free SWAR form
-// ((x | 0x80..) - 0x08..) ^ (~x & 0x80..).  One lane per dword pair.  The first
-// nsc lanes also write the GEMM's bf16 split of one activation scale each
-// (split_scale_bf16x3; nsc = rows * K/128 never exceeds the lane count).
+// ((x | 0x80..) - 0x08..) ^ (~x & 0x80..).  One lane per dword pair.
 __device__ __forceinline__ uint32_t swar_sub8(uint32_t x) {
     return ((x | 0x80808080u) - 0x08080808u) ^ (~x & 0x80808080u);
 }
@@ -229,11 +227,8 @@ __device__ __forceinline__ uint32_t swar_sub8(uint32_t x) {
 template <bool HAS_H>
 __global__ __launch_bounds__(256) void hl_to_i8_k(const uint32_t* __restrict__ qh,
                                                   const uint32_t* __restrict__ ql,
-                                                  int8_t* __restrict__ xq, size_t ndw,
-                                                  const float* __restrict__ sc, uint4* __restrict__ sc_split,
-                                                  size_t nsc) {
+                                                  int8_t* __restrict__ xq, size_t ndw) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < nsc) sc_split[i] = split_scale_bf16x3(sc[i]);
     if (i >= ndw) return;
     const uint32_t h = HAS_H ? qh[i] : 0u, l = ql[i] ^ 0x88888888u;
     const uint32_t xe = ((h << 4) & 0xF0F0F0F0u) | (l & 0x0F0F0F0Fu);
@@ -242,14 +237,13 @@ __global__ __launch_bounds__(256) void hl_to_i8_k(const uint32_t* __restrict__ q
 }
 
 hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
-                           hipStream_t st, const float* sc, uint4* sc_split) {
+                           hipStream_t st) {
     const size_t ndw = (size_t)rows * (K / 8);
-    const size_t nsc = sc && sc_split ? (size_t)rows * (K / 128) : 0;
     const unsigned blocks = (unsigned)((ndw + 255) / 256);
     if (qh)
-        hipLaunchKernelGGL(hl_to_i8_k<true>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw, sc, sc_split, nsc);
+        hipLaunchKernelGGL(hl_to_i8_k<true>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
     else  // int4 codes alone (W4A4): sign-extended into the same interleaved int8 order
-        hipLaunchKernelGGL(hl_to_i8_k<false>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw, sc, sc_split, nsc);
+        hipLaunchKernelGGL(hl_to_i8_k<false>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
     return hipGetLastError();
 }
 

@@ -20,10 +20,8 @@ hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc
 hipError_t launch_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
                                 int in_stride, int in_off, hipStream_t st);
 // q8 = 16h + l from digit planes, or the sign-extended l alone when qh is null.
-// With sc and sc_split, the same launch also writes the prefill GEMM's bf16 splits
-// of the rows * K/128 activation scales sc (launch_split_scales).
 hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
-                           hipStream_t st, const float* sc = nullptr, uint4* sc_split = nullptr);
+                           hipStream_t st);
 hipError_t launch_quant_act_a4(uint32_t* aq, float* sa, const float* x, int rows, int K, hipStream_t st);
 hipError_t launch_make_group_major(float* out, const uint16_t* ws, int N, int NG, hipStream_t st);
 
@@ -69,9 +67,7 @@ hipError_t launch_gemv_w4a4(float* y, const uint32_t* wq, const uint16_t* ws, co
 
 // ---- prefill GEMM (gemm.hip)
 // C f32 [M][N] from int8 codes A [M][K] (interleaved), RT4 weights W [N][K/8],
-// group-major scales: the activation scales as their bf16 splits sa [K/128][M]
-// (launch_split_scales) and the weight scales sb [K/128][N] (fp16 values widened
-// to fp32, as make_group_major writes them); gsum (optional, tests)
+// group-major scales sa [K/128][M] and sb [K/128][N]; gsum (optional, tests)
 // receives the exact per-group int32 dot products [M][N][K/128].  The launch is
 // persistent (one workgroup per CU, equal shares of the (tile, group) units);
 // `part` and `cnt` are its split-tile workspace: part_bytes of partial sums and
@@ -84,10 +80,8 @@ struct GemmPlan {
 };
 GemmPlan gemm_plan(int M, int N, int K, int cus);
 hipError_t launch_gemm_w4a8(float* C, int32_t* gsum, const int8_t* A, const uint32_t* W,
-                            const uint4* sa, const float* sb, int M, int N, int K, const GemmPlan& plan,
+                            const float* sa, const float* sb, int M, int N, int K, const GemmPlan& plan,
                             float* part, int* cnt, hipStream_t st);
-// out[i] = the bf16 split of s[i] (split_scale_bf16x3), i < n.
-hipError_t launch_split_scales(uint4* out, const float* s, size_t n, hipStream_t st);
 hipError_t launch_zero_i32(int* p, size_t n, hipStream_t st);
 
 // ---- int4-KV attention (attn.hip); head dim 256, Q/K groups of 128, V tiles of 64 keys
