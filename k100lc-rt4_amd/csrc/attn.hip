@@ -39,7 +39,9 @@
 // which leaves its state bit-for-bit unchanged.  The tile loop is a two-tile
 // pipeline (S and P of the next tile beside the PV product of the current one;
 // see the loop), the scale products of both contractions run on
-// v_mfma_f32_4x4x1f32, and K/V are read with range-checked buffer loads.
+// v_mfma_f32_16x16x1f32 (four 16x16 tiles per instruction: 2 per tile for S, 4
+// for O; four v_mfma_f32_4x4x1f32 cost about twice the matrix-core time of one),
+// and K/V are read with range-checked buffer loads.
 #include <type_traits>
 
 #include "rt4_dev.h"
@@ -66,14 +68,16 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int key_of_slot(int G, int r) { return 8 * (G >> 1) + 2 * r + (G & 1); }
 __device__ __forceinline__ int slot_of_key(int k) { return 4 * (2 * (k >> 3) + (k & 1)) + ((k & 7) >> 1); }
 
-// Products x[4G + r] * y for r = 0..3 in the 16x16 accumulator layout (lane l =
-// 16G + i holds rows 4G..4G+3 of column i), on the matrix core: v_mfma_f32_4x4x1
-// gives lane l, output r, the A operand of lane 4(l/4) + r times the B operand of
-// lane l, so A = x[4G + (l & 3)] and B = the lane's own y.  Each output is the one
-// fp32 rounding of the product, as a v_mul_f32 would give.
-__device__ __forceinline__ v4f outer4(float x_of_lane, float y) {
-    const v4f z = {0.f, 0.f, 0.f, 0.f};
-    return __builtin_amdgcn_mfma_f32_4x4x1f32(x_of_lane, y, z, 0, 0, 0);
+// Products x[4G + r] * y[i] for four 16x16 tiles b in their accumulator layout
+// (lane l = 16G + i holds rows 4G..4G+3 of column i, tile b in registers 4b..4b+3),
+// on the matrix core: v_mfma_f32_16x16x1f32 (four blocks, k = 1) gives lane l,
+// register 4b + r, the A operand of lane 16b + 4(l >> 4) + r times the B operand of
+// lane 16b + (l & 15) (lane layout checked on the card), so tile b's x[j] comes
+// from lane 16b + j and every lane supplies its own column's y.  Each output is the
+// one fp32 rounding of the product, as a v_mul_f32 would give.
+__device__ __forceinline__ v16f outer16(float x_of_lane, float y) {
+    const v16f z = {};
+    return __builtin_amdgcn_mfma_f32_16x16x1f32(x_of_lane, y, z, 0, 0, 0);
 }
 
 __device__ __forceinline__ int sext4(uint32_t w, int e) { return ((int)(w << (28 - 4 * e))) >> 28; }
@@ -313,10 +317,10 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 
     const int tid = threadIdx.x, lane = tid & 63, w = uniform(tid >> 6);
     const int qi = lane & 15, G = lane >> 4;
-    // the key (within a subtile) whose scale this lane supplies to the scale products:
-    // outer4 gives lane l, output r, the operand of lane 4(l/4) + r, i.e. of register r
-    // of lane group G
-    const int kslot = key_of_slot(G, lane & 3);
+    // the key whose scale this lane supplies to the S scale products: outer16 gives
+    // lane l, register 4kt + r, the operand of lane 16kt + 4(l >> 4) + r, so lane j
+    // supplies the key of register j & 3 of lane group (j >> 2) & 3 in subtile j >> 4
+    const int kslot = 16 * G + key_of_slot((lane >> 2) & 3, lane & 3);
     const int head = blockIdx.y, vh = head / ratio;
     const int q0 = blockIdx.x * QROWS;
     const int qrow = q0 + 16 * w + qi;
@@ -456,6 +460,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const unsigned char* kub = ku + b * KU_BYTES;
         const float* ksb = ks_l[b];
         float sv[4][4];
+        // key scale x query scale of every entry (subtile kt in registers 4kt..4kt+3)
+        const v16f c0 = outer16(ksb[kslot], A0);
+        const v16f c1 = outer16(ksb[BNK + kslot], A1);
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             const v4i* kp = reinterpret_cast<const v4i*>(kub) + (kt * 4) * 64 + lane;
@@ -463,11 +470,8 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[64], qop[1], a0, 0, 0, 0);
             v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
             a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
-            // key scale x query scale of each entry, then S = a1 * c1 + a0 * c0
-            const v4f c0 = outer4(ksb[16 * kt + kslot], A0);
-            const v4f c1 = outer4(ksb[BNK + 16 * kt + kslot], A1);
 #pragma unroll
-            for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[r], (float)a0[r] * c0[r]);
+            for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[4 * kt + r], (float)a0[r] * c0[4 * kt + r]);
         }
         if constexpr (MASK) {
             if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
@@ -551,12 +555,16 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const unsigned char* vub = vu + b * VU_BYTES;
         const float* vsb = vs_l[b];
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
-            const v4i va = *(reinterpret_cast<const v4i*>(vub) + dt * 64 + lane);
-            const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pop, zero, 0, 0, 0);
-            const v4f ps = outer4(vsb[16 * dt + 4 * G + (lane & 3)], pb16);   // vsc * pb16
+        for (int dq = 0; dq < 4; dq++) {
+            const v16f ps = outer16(vsb[64 * dq + lane], pb16);   // vsc * pb16 of dim tiles 4dq..4dq+3
 #pragma unroll
-            for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], ps[r], O[dt][r]);
+            for (int d4 = 0; d4 < 4; d4++) {
+                const int dt = 4 * dq + d4;
+                const v4i va = *(reinterpret_cast<const v4i*>(vub) + dt * 64 + lane);
+                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(va, pop, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], ps[4 * d4 + r], O[dt][r]);
+            }
         }
     };
 
