@@ -162,3 +162,32 @@ def test_gemm_tail_tiles_with_continuing_workgroups(rt4, orc, torch_gpu, entry, 
     worst = float(np.abs(got - ref).max()) / rms
     print(f"  rel_l2 = {err:.3e}  worst/rms = {worst:.3e}")
     assert err < TIGHT and worst < 1e-5
+
+
+def test_gemm_scale_products_over_wide_exponent_range(rt4, orc, torch_gpu):
+    """The scale products sa*sb come from exact bf16 splits of both scales (three
+    parts of sa, two of the fp16-valued sb).  Activation scales spanning 2^-40 ..
+    2^40 across rows and groups exercise every exponent the splits see; each row
+    must match the fp64 oracle to fp32 accuracy on its own (a per-row relative L2,
+    so small rows are not hidden behind large ones), for both entries."""
+    M, N, K = 256, 320, 1024
+    print(f"case gemm scale range M={M} N={N} K={K}", flush=True)
+    c = workload.gemm_case(41, M, N, K)
+    rng = np.random.default_rng(41)
+    er = rng.integers(-40, 41, M).astype(np.float64)
+    eg = rng.integers(-8, 9, K // 128).astype(np.float64)
+    c["x"] = (c["x"] * np.exp2(er)[:, None] * np.repeat(np.exp2(eg), 128)[None, :]).astype(np.float32)
+    wq, ws, x = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["ws"]), dev(torch_gpu, c["x"])
+    sb = rt4.make_group_major(ws, K)
+    xq, sc8 = rt4.quant_rows_i8(x)
+    y8 = host(rt4.gemm_w4a8_i8(wq, sb, xq, sc8))
+    qh, ql, sc, sc16 = rt4.quant_rows_a8(x)
+    y = host(rt4.gemm_w4a8(wq, sb, qh, ql, sc, sc16))
+    assert np.array_equal(y.view(np.uint32), y8.view(np.uint32)), "digit-plane and int8 entries differ"
+    mi = np.repeat(np.arange(M), N).astype(np.int32)
+    ni = np.tile(np.arange(N), M).astype(np.int32)
+    ref, _ = _oracle_points(orc, c, M, N, K, mi, ni)
+    ref = ref.reshape(M, N)
+    worst = max(rel_l2(y8[m], ref[m]) for m in range(M))
+    print(f"  worst per-row rel_l2 = {worst:.3e}")
+    assert worst < TIGHT
