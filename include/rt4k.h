@@ -63,6 +63,17 @@ const char* rt4_last_error(void);
 /* ABI version of this header (bumped on incompatible change). */
 int rt4_abi_version(void);
 
+/* Frees the library scratch of the current device: the buffers in use and every
+ * outgrown one kept for graphs captured earlier.  Waits for the device first
+ * (hipDeviceSynchronize), so no call already issued can still use them; the next
+ * call that needs scratch allocates it again.  Graphs captured before this call
+ * must not be replayed afterwards (they would write into freed memory): call it
+ * when such graphs are destroyed or at shutdown.  The static array of
+ * rt4_gemv_w4a8_noalloc is not affected.  Not a graph operation (fails under
+ * capture through hipDeviceSynchronize).  No reference counterpart: the
+ * reference frees its scratch only when it grows (src/k_gemv.hip:16-23). */
+int rt4_release_scratch(void);
+
 /* ------------------------------------------------------------ decode path -- */
 
 /* Decode-side activation quantizer.  Replaces the quant_act launch of

@@ -4,6 +4,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
+#include <vector>
 
 #include "rt4_internal.h"
 #include "rt4k.h"
@@ -42,6 +43,7 @@ struct Buf {
 };
 std::mutex g_mu;
 Buf g_buf[kMaxDev][kSlots];
+std::vector<void*> g_retired[kMaxDev];   // outgrown buffers, freed only by rt4_release_scratch
 
 // Whether this device's scratch slot already holds at least `bytes`.
 bool scratch_has(Slot slot, size_t bytes) {
@@ -81,7 +83,8 @@ int lib_scratch(Slot slot, size_t bytes, void** out, hipStream_t st, bool zero =
         void* p = nullptr;
         e = hipMalloc(&p, want);
         if (e != hipSuccess) return hip_status(e, "hipMalloc(scratch)");
-        b.p = p;            // the outgrown buffer, if any, stays allocated (see above)
+        if (b.p) g_retired[dev].push_back(b.p);   // outgrown: stays allocated (see above)
+        b.p = p;
         b.cap = want;
         if (zero) {
             e = rt4::launch_zero_i32(static_cast<int*>(b.p), want / sizeof(int), st);
@@ -328,6 +331,32 @@ extern "C" {
 
 const char* rt4_last_error(void) { return g_err; }
 int rt4_abi_version(void) { return 1; }
+
+int rt4_release_scratch(void) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDev) return fail(RT4_E_ARG, "device %d out of range", dev);
+    // every call already issued on any stream of this device may still use the buffers
+    e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_status(e, "hipDeviceSynchronize");
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (void* p : g_retired[dev]) {
+        e = hipFree(p);
+        if (e != hipSuccess) return hip_status(e, "hipFree(retired scratch)");
+    }
+    g_retired[dev].clear();
+    for (int s = 0; s < kSlots; s++) {
+        Buf& b = g_buf[dev][s];
+        if (b.p) {
+            e = hipFree(b.p);
+            if (e != hipSuccess) return hip_status(e, "hipFree(scratch)");
+        }
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    return RT4_OK;
+}
 
 int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K,
                      void* stream) {

@@ -27,7 +27,7 @@ GROUP = 128
 
 # Every symbol include/rt4k.h declares (checked by the CPU test suite).
 C_EXPORTS = (
-    "rt4_last_error", "rt4_abi_version",
+    "rt4_last_error", "rt4_abi_version", "rt4_release_scratch",
     "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
     "rt4_gemv_w4a8_groupsums",
     "rt4_gemv_w4a8", "rt4_gemv_w4a8_noalloc", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
@@ -114,6 +114,8 @@ def lib() -> ctypes.CDLL:
         L.rt4_last_error.restype = ctypes.c_char_p
         L.rt4_last_error.argtypes = []
         L.rt4_abi_version.restype = ctypes.c_int
+        L.rt4_release_scratch.restype = ctypes.c_int
+        L.rt4_release_scratch.argtypes = []
         for name, args in _SIGS.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -125,6 +127,13 @@ def lib() -> ctypes.CDLL:
 def _check(rc: int) -> None:
     if rc != 0:
         raise RT4Error(lib().rt4_last_error().decode(errors="replace"))
+
+
+def release_scratch() -> None:
+    """Free the library scratch of the current device (see rt4_release_scratch in
+    include/rt4k.h): waits for the device; graphs captured earlier must not be
+    replayed afterwards."""
+    _check(lib().rt4_release_scratch())
 
 
 # ----------------------------------------------------------- torch helpers --

@@ -10,6 +10,9 @@ Nothing may be allocated while a stream is being captured.  In a fresh process
 * the attention prefill with an automatic split count: it falls back to one
   split (no workspace) and every replay equals the eager one-split result.
 
+Then it frees the library scratch (rt4_release_scratch): the GEMM capture fails
+again until an eager call re-allocates it, and the re-run calls are bit-identical.
+
 Each replay is preceded by eager work and a synchronisation, and checked bit for
 bit.  The child process runs the whole sequence and prints one line per check.
 """
@@ -112,6 +115,23 @@ CHILD = textwrap.dedent(r"""
     print(f"attention captured without workspace = one split; eager automatic split vs one split {{rel:.2e}}",
           flush=True)
     assert rel < 1e-5
+
+    # ---- release the scratch: capture needs an eager call again, results unchanged
+    del g
+    rt4_amd.release_scratch()
+    g, err = capture(lambda: rt4_amd.gemm_w4a8_i8(wq, sb, xq, sc, out=c))
+    print("gemm capture after release:", err, flush=True)
+    assert err is not None and "captur" in err, err
+    again = rt4_amd.gemm_w4a8_i8(wq, sb, xq, sc).clone()
+    againv = rt4_amd.gemv_w4a8(wq2, ws2, xa).clone()
+    againa = rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, **kw).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(again.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(againv.view(torch.int32), wantv.view(torch.int32))
+    assert torch.equal(againa.view(torch.int32), auto.view(torch.int32))
+    rt4_amd.release_scratch()
+    rt4_amd.release_scratch()   # nothing left to free: still fine
+    print("release: re-allocated scratch gives bit-identical GEMM, GEMV and attention", flush=True)
     print("CAPTURE-OK", flush=True)
 """)
 
