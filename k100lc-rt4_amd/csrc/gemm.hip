@@ -493,8 +493,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
 #pragma unroll
         for (int s2 = 0; s2 < 2; s2++) bp[s2] = *reinterpret_cast<const uint4*>(lds + rb[s2]);
     };
+    // the scale operands of a unit, read once its stage is valid (right after the
+    // barrier that follows its split) so the scale MFMAs never wait for a fresh LDS
+    // read: sb of this wave's column and the sa splits of the four row tiles
+    v4h sap[4];
+    float sbr;
+    auto read_s = [&]() __attribute__((always_inline)) {
+        sbr = *reinterpret_cast<const float*>(lds + rsb);
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) sap[ii] = sa_of(ii);
+    };
     read_a(a_cur, 0);
     read_b();
+    read_s();
 
     // Software pipeline over row tiles: the MFMAs of row tile t run while tile t-1
     // is folded.  The last tile of a unit is folded during the first tile of the
@@ -533,19 +544,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // row tile 0, with the unpack of this unit's weights and the fold of the
         // previous unit's last tile
         read_a(a_nxt, 1);
-        const v4h sbz = split_sb(*reinterpret_cast<const float*>(lds + rsb), lh);
+        const v4h sbz = split_sb(sbr, lh);
         // (for the first unit of a segment accB is zero: the fold adds exact zeros)
         step(a_cur, accA, accB, facc[3], 3, xprev, true, true);
-        S = scales(sa_of(0), sbz);
+        S = scales(sap[0], sbz);
         // row tile 1, fold of tile 0
         read_a(a_cur, 2);
         step(a_nxt, accB, accA, facc[0], 0, x, false, true);
-        S = scales(sa_of(1), sbz);
+        S = scales(sap[1], sbz);
         // row tile 2, fold of tile 1
         read_a(a_nxt, 3);
         step(a_cur, accA, accB, facc[1], 1, x, false, true);
-        S = scales(sa_of(2), sbz);
-        const v4h sa3 = sa_of(3);   // read before the barrier: the stage is refilled after it
+        S = scales(sap[2], sbz);
+        const v4h sa3 = sap[3];     // sap is refilled with the next unit's after the barrier
         // row tile 3.  The DMA of unit i+1 has landed once at most the two younger
         // units' loads are pending (three units in flight), and every wave has issued
         // its last read of this stage (the barrier waits for LDS reads).  Near the
@@ -564,6 +575,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         next_stage((st + 1) & (NS - 1));
         read_b();
         read_a(a_cur, 0);
+        read_s();
         step(a_nxt, accB, accA, facc[2], 2, x, false, true);
         S = scales(sa3, sbz);
         ++i;
@@ -588,6 +600,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // leaves the flush the registers it needs
         read_b();
         read_a(a_cur, 0);
+        read_s();
         // next tile
         ++cur.t;
         cur.bm += BM;
