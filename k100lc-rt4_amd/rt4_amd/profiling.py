@@ -20,7 +20,9 @@ SQ counters per run):
         SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY GRBM_GUI_ACTIVE --output-format csv -d <dir> -o sqb \
         -- python3 bench.py --pmc-probe
 
-and `python -m rt4_amd.profiling sq <sqa.csv> <sqb.csv> <out.json>` writes the
+`python -m rt4_amd.profiling trace <kernel_trace.csv>` prints the per (kernel,
+launch grid) duration table of a `rocprofv3 --kernel-trace` run, and
+`python -m rt4_amd.profiling sq <sqa.csv> <sqb.csv> <out.json>` writes the
 mean per dispatch of every counter for each kernel of KERNELS, with the derived
 fractions: MFMA busy (SQ_VALU_MFMA_BUSY_CYCLES, summed over the SIMDs, per SIMD
 per cycle of the dispatch; GRBM_GUI_ACTIVE is summed over the XCDs, 32 CUs
@@ -131,7 +133,39 @@ def summarize_sq(paths: list[str], cus: int) -> dict:
     return res
 
 
+def kernel_table(path: str, needles: tuple[str, ...] = ("rt4::", "read_burst_k", "mfma_i8_k", COPY_KERNEL)) -> list[dict]:
+    """Per (kernel, launch grid) duration statistics in microseconds from a rocprofv3
+    kernel trace (`--kernel-trace --output-format csv`), for the kernels whose name
+    contains one of `needles` (this library, the probes), ordered by total time."""
+    groups: dict[tuple, list[float]] = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"]
+            if not any(n in name for n in needles):
+                continue
+            wg = int(row["Workgroup_Size_X"])
+            gx, gy = int(row["Grid_Size_X"]) // wg, int(row["Grid_Size_Y"]) // max(1, int(row["Workgroup_Size_Y"]))
+            short = name.replace("(anonymous namespace)::", "").split("(")[0]
+            short = short[5:] if short.startswith("void ") else short
+            us = (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1000.0
+            groups.setdefault((short, gx, wg, gy), []).append(us)
+    rows = []
+    for (short, gx, wg, gy), v in groups.items():
+        rows.append({"kernel": short, "grid": f"{gx} x {wg}" + (f" (y {gy})" if gy > 1 else ""), "calls": len(v),
+                     "avg": statistics.fmean(v), "median": statistics.median(v), "min": min(v), "max": max(v),
+                     "total": sum(v)})
+    rows.sort(key=lambda r: -r["total"])
+    return rows
+
+
 def main(argv: list[str]) -> int:
+    if len(argv) == 3 and argv[1] == "trace":
+        print("| kernel | grid | calls | avg us | median us | min us | max us |")
+        print("|---|---|---|---|---|---|---|")
+        for r in kernel_table(argv[2]):
+            print(f"| `{r['kernel']}` | {r['grid']} | {r['calls']} | {r['avg']:.2f} | {r['median']:.2f} | "
+                  f"{r['min']:.2f} | {r['max']:.2f} |")
+        return 0
     if len(argv) >= 2 and argv[1] == "sq":
         if len(argv) != 5:
             print(__doc__, file=sys.stderr)

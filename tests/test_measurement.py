@@ -90,6 +90,29 @@ def test_sq_summary_fractions(tmp_path):
     assert d["per_wave_valu"] == 300 and d["per_wave_mfma"] == 20
 
 
+def test_kernel_table_groups_by_kernel_and_grid(tmp_path):
+    from rt4_amd import profiling
+    cols = ["Kind", "Kernel_Name", "Start_Timestamp", "End_Timestamp", "Workgroup_Size_X", "Workgroup_Size_Y",
+            "Grid_Size_X", "Grid_Size_Y"]
+    gemv = "void rt4::(anonymous namespace)::gemv_w4a8_k<4, 2, 1, true, false, false, true>(unsigned int const*)"
+    probe = "void (anonymous namespace)::read_burst_k<6, true>(uint4 const*, int)"
+    other = "void at::native::vectorized_elementwise_kernel<4, at::native::float16_copy_kernel_cuda>(int)"
+    rows = [(gemv, 0, 10_000, 256, 1, 1280 * 256, 1), (gemv, 0, 12_000, 256, 1, 1280 * 256, 1),
+            (gemv, 0, 30_000, 1024, 1, 512 * 1024, 1),            # another launch grid: its own row
+            (probe, 0, 8_000, 512, 1, 1024 * 512, 1), (other, 0, 99_000, 256, 1, 256, 1)]
+    with open(tmp_path / "t.csv", "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(cols)
+        for name, t0, t1, wg, wgy, gx, gy in rows:
+            w.writerow(["KERNEL_DISPATCH", name, t0, t1, wg, wgy, gx, gy])
+    tab = profiling.kernel_table(str(tmp_path / "t.csv"))
+    assert [(r["kernel"], r["grid"], r["calls"]) for r in tab] == [
+        ("rt4::gemv_w4a8_k<4, 2, 1, true, false, false, true>", "512 x 1024", 1),
+        ("rt4::gemv_w4a8_k<4, 2, 1, true, false, false, true>", "1280 x 256", 2),
+        ("read_burst_k<6, true>", "1024 x 512", 1)]          # torch's kernels are left out
+    assert tab[1]["avg"] == pytest.approx(11.0) and tab[1]["min"] == pytest.approx(10.0)
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
