@@ -37,8 +37,10 @@
 // (scalar, vector, LDS; an int8 MFMA takes about 16), with little overlap
 // between the two waves, and the fold alone is two vector instructions per
 // output per group (128 per wave per unit against 16 MFMAs).  So the
-// loop is built for few instructions: it is unrolled over the four LDS stages so
-// that every LDS address is a per-lane register plus an immediate offset; the DMA
+// loop is built for few instructions: every LDS read address is a per-lane
+// register (moved on by one stage per unit, one add per register) plus the row
+// tile as an immediate offset (a body unrolled over the four stages, which would
+// make the stage an immediate too, spilled around the flush); the DMA
 // sources are per-lane offsets (fixed while the tile is unchanged) plus scalar
 // base pointers advanced by a constant per unit; tile bookkeeping is a few
 // scalar counters.  The MFMAs of a row tile are interleaved one by one with the
@@ -237,7 +239,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     const int n = (int)(u1 - u0);
     const int first_tile = (int)(u0 / NG);
 
-    // per-lane LDS read offsets; stage, row tile and pair are immediates
+    // per-lane LDS read offsets into the current stage (next_stage moves them on);
+    // the row tile is an immediate
     int ra[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) ra[ks] = LDS_A + lr * 128 + (((4 * (ks >> 1) + 2 * lh + (ks & 1)) ^ ((lr >> 1) & 7)) * 16);
