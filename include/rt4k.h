@@ -13,9 +13,10 @@
  * buffer per device and kind, grown on demand like the reference's static
  * scratch (src/k_gemv.hip:16-23).  Calls that may run at the same time on one
  * device (different streams) therefore race on it; the caller orders them, as
- * it must for the reference.  An outgrown buffer is kept allocated until the
- * process ends (the reference frees it), so a HIP graph captured before a
- * larger call still replays into valid memory; growth is by half at least.
+ * it must for the reference.  An outgrown buffer is kept allocated until
+ * rt4_release_scratch or the end of the process (the reference frees it on
+ * growth), so a HIP graph captured before a larger call still replays into valid
+ * memory; growth is by half at least.
  * Nothing is allocated while `stream` is being captured: a call that would
  * have to grow a scratch buffer then fails with RT4_E_CAPTURE, except that the
  * split GEMV and the attention prefill (automatic split count) fall back to
