@@ -517,22 +517,20 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     // Accumulators with fixed roles: row tiles 0 and 2 of a unit go to accA, tiles
     // 1 and 3 to accB, and a fold reads the one the MFMAs are not writing (no copies).
     v16i accA, accB;
-    v16f S;              // scale products of the row tile being folded
+    v16f Se, So;         // scale products of the even and odd row tiles
     // One row-tile step: the four MFMAs of tile (a, bu) into acc, each followed by a
-    // quarter of the fold of the previous tile (prev into facc[fi]) and, with
-    // UNPACK, by the unpack of the next k-step's weights; with LATE the fold starts
-    // one MFMA later (its scale products are still being formed).
+    // quarter of the fold of the previous tile (prev into facc[fi], with its scale
+    // products S, formed one row tile earlier) and, with UNPACK, by the unpack of
+    // the next k-step's weights.
     auto step = [&](const v4i (&a)[4], v16i& acc, const v16i& prev, v16i& fa, int fi, const TileRef& fx,
-                    bool do_unpack, bool late) __attribute__((always_inline)) {
+                    bool do_unpack, const v16f& S) __attribute__((always_inline)) {
         if (do_unpack) unpack_ks(bu, bp, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks], bu[ks], ks ? acc : zero16, 0, 0, 0);
             if (do_unpack && ks < 3) unpack_ks(bu, bp, ks + 1);
-            if (!late) fold_q(fa, prev, S, fi, ks, fx);
-            else if (ks == 1) { fold_q(fa, prev, S, fi, 0, fx); fold_q(fa, prev, S, fi, 1, fx); }
-            else if (ks > 1) fold_q(fa, prev, S, fi, ks, fx);
+            fold_q(fa, prev, S, fi, ks, fx);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -548,18 +546,22 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // previous unit's last tile
         read_a(a_nxt, 1);
         const v4h sbz = split_sb(sbr, lh);
+        // The scale products of each row tile are formed before its MFMAs, in the
+        // buffer of its parity (even tiles Se, odd So), so they are ready long
+        // before the tile is folded during the next row tile (configs[2]: ~1-2%
+        // against forming them after the MFMAs and starting the fold one MFMA late).
         // (for the first unit of a segment accB is zero: the fold adds exact zeros)
-        step(a_cur, accA, accB, facc[3], 3, xprev, true, true);
-        S = scales(sap[0], sbz);
+        Se = scales(sap[0], sbz);
+        step(a_cur, accA, accB, facc[3], 3, xprev, true, So);
+        So = scales(sap[1], sbz);
         // row tile 1, fold of tile 0
         read_a(a_cur, 2);
-        step(a_nxt, accB, accA, facc[0], 0, x, false, true);
-        S = scales(sap[1], sbz);
+        step(a_nxt, accB, accA, facc[0], 0, x, false, Se);
+        Se = scales(sap[2], sbz);
         // row tile 2, fold of tile 1
         read_a(a_nxt, 3);
-        step(a_cur, accA, accB, facc[1], 1, x, false, true);
-        S = scales(sap[2], sbz);
-        const v4h sa3 = sap[3];     // sap is refilled with the next unit's after the barrier
+        step(a_cur, accA, accB, facc[1], 1, x, false, So);
+        So = scales(sap[3], sbz);   // before the barrier: sap is refilled with the next unit's after it
         // row tile 3.  The DMA of unit i+1 has landed once at most the two younger
         // units' loads are pending (three units in flight), and every wave has issued
         // its last read of this stage (the barrier waits for LDS reads).  Near the
@@ -579,8 +581,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         read_b();
         read_a(a_cur, 0);
         read_s();
-        step(a_nxt, accB, accA, facc[2], 2, x, false, true);
-        S = scales(sa3, sbz);
+        step(a_nxt, accB, accA, facc[2], 2, x, false, Se);
         ++i;
         if (GSUM) ++cur.g;
     };
@@ -590,13 +591,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const int len = min(NG - g0, n - i);
         if (GSUM) cur.g = g0;
         accB = zero16;
-        S = zero16f;
+        So = zero16f;
         for (int k = 0; k < len; k++) unit(k == 0);
         // the segment's last row tile 3, then publish the segment
         TileRef xl = cur;
         if (GSUM) xl.g = cur.g - 1;
 #pragma unroll
-        for (int q = 0; q < 4; q++) fold_q(facc[3], accB, S, 3, q, xl);
+        for (int q = 0; q < 4; q++) fold_q(facc[3], accB, So, 3, q, xl);
         flush(cur);
         // the next unit's fragments, read again from its stage (still intact): the
         // copies read during the last unit are then dead across the flush, which
