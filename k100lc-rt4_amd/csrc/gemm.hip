@@ -41,9 +41,9 @@
 // register (moved on by one stage per unit, one add per register) plus the row
 // tile as an immediate offset (a body unrolled over the four stages, which would
 // make the stage an immediate too, spilled around the flush); the DMA
-// sources are per-lane offsets (fixed while the tile is unchanged) plus scalar
-// base pointers advanced by a constant per unit; tile bookkeeping is a few
-// scalar counters.  The MFMAs of a row tile are interleaved one by one with the
+// sources are the kernel's scalar base pointers plus per-lane 32-bit offsets,
+// moved on by one group per unit (advancing the scalar bases instead measured
+// the same); tile bookkeeping is a few scalar counters.  The MFMAs of a row tile are interleaved one by one with the
 // fold of the previous row tile (and with the unpack of the next k-step), in an
 // order the compiler may not change (sched_barrier; every folded value also
 // passes through an empty asm statement where it is formed, without which the
