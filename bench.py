@@ -571,6 +571,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         kernels.update(gemm_table(torch, rt4_amd, workload, gen))
         kernels.update(attn_table(torch, rt4_amd, workload, gen))
+        # the same figures against the int8 MFMA issue rate measured on this box for the
+        # instruction each kernel runs (the GEMM 32x32x32, the attention 16x16x64)
+        for key, rate in (("gemm_c2_gate_up", "mfma_i32_32x32x32_i8_TOPS"),
+                          ("gemm_c2_down", "mfma_i32_32x32x32_i8_TOPS"),
+                          ("attn_c4_prefill", "mfma_i32_16x16x64_i8_TOPS")):
+            tops = kernels[key].get("TOPS", kernels[key].get("TOPS_effective"))
+            kernels[key]["frac_measured_issue"] = round(tops / kernels["ceilings"][rate], 4)
         lm = [workload.weights_torch(248320, 5120, generator=gen) for _ in range(2)]
         y_lm = torch.empty((M, 248320), device="cuda")
 
