@@ -396,14 +396,19 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vsc), 0, (kv_cap / BNK) * HD * 4, kRsrcW3);
     const int off_k = ((tid & 63) * KDW + 8 * (tid >> 6)) * 4;          // + tile * BNK * KDW * 4
     const int off_ks = (((tid >> 6) & 1) * kv_cap + (tid & 63)) * 4;    // + tile * BNK * 4
+    // Tile byte offsets are formed in 32-bit unsigned arithmetic: the prefetch reads
+    // up to three tiles past the last one, and at the largest accepted cache
+    // (kv_cap = 2^24 - 64) that tile's K offset is 2^31, beyond int.  The range check
+    // compares the unsigned offset with the resource's size, so such a tile reads
+    // zeros (checked on the CPU by tests/test_attention.py).
     auto load_k = [&](StageK& S, int t) {
-        const int sk = t * (BNK * KDW * 4);
+        const int sk = (int)((uint32_t)t * (uint32_t)(BNK * KDW * 4));
         S.k0 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k, sk, 0);
         S.k1 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k + 16, sk, 0);
         S.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_ks, off_ks, t * BNK * 4, 0));
     };
     auto load_v = [&](StageV& S, int t) {
-        const int sv = t * (BNK / 8 * HD * 4);
+        const int sv = (int)((uint32_t)t * (uint32_t)(BNK / 8 * HD * 4));
 #pragma unroll
         for (int g = 0; g < 8; g++)
             S.v[g] = __builtin_amdgcn_raw_buffer_load_b32(rs_v, tid * 4 + (g & 3) * HD * 4,

@@ -54,10 +54,19 @@ bool scratch_has(Slot slot, size_t bytes) {
 }
 
 // Whether work on `st` is being recorded into a HIP graph (nothing may be
-// allocated then: hipMalloc is not a graph operation).
+// allocated then: hipMalloc is not a graph operation).  A failed query counts as
+// not capturing, so that work after a capture the runtime invalidated can still
+// allocate.  (Measured on ROCm 7.2: asked about the legacy stream while another
+// stream captures in global mode, the query reports no capture; the hipMalloc
+// that follows is refused by the runtime, so such a call fails with RT4_E_HIP
+// having allocated nothing -- using the legacy stream there is the caller's
+// error under global capture, which invalidates that capture in any case.)
 bool capturing(hipStream_t st) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess) return false;
+    if (hipStreamIsCapturing(st, &cap) != hipSuccess) {
+        (void)hipGetLastError();   // not left for the caller's next HIP call
+        return false;
+    }
     return cap != hipStreamCaptureStatusNone;
 }
 

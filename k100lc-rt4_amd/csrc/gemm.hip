@@ -26,9 +26,10 @@
 // the accumulator layout.  Its operands are exact bf16 splits: sa = b1 + b2 + b3
 // (three bf16 values, 3 x 8 significant bits holding fp32's 24, made per unit by
 // the two waves that load sa, one row per lane, into LDS before the unit's
-// barrier) and sb = c1 + c2 (RT4 weight scales are fp16 values, 11
-// significant bits), so the six products b_i * c_j are exact and the MFMA's
-// fp32 sum of them is sa * sb to within a few units in the last place.  The
+// barrier) and sb = c1 + c2 + c3 (the same split of the fp32 weight scale; the
+// RT4 scales are fp16 values, which leave c3 = 0), so the eight products b_i *
+// c_j other than b3 * c3 (below 2^-32 of sa * sb) are exact and the MFMA's fp32
+// sum of them is sa * sb to within a few units in the last place.  The
 // bf16 MFMA occupies the matrix core ~15 cycles against ~70 for the fp32 one
 // (v_mfma_f32_32x32x2_f32 with its k = 1 half zero), measured.
 //
@@ -78,14 +79,20 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef short v4h __attribute__((ext_vector_type(4)));   // four bf16 bit patterns (MFMA operand)
 
-// sb = c1 + c2 with c1 its bf16 truncation and c2 the exact rest (an fp16 value has
-// 11 significant bits, so the rest has at most 3), as the B operand of the scale
-// MFMA: (c1, c2, c1, c2) in lanes 0..31, (c1, c2, 0, 0) in lanes 32..63.
-__device__ __forceinline__ v4h split_sb(float sb, int lh) {
+// sb = c1 + c2 + c3, each the bf16 truncation of what is left (fp32's 24
+// significant bits in 3 x 8; an fp16-valued sb leaves c3 = 0), as the B operand of
+// the scale MFMA: (c1, c2, c3, c1) in lanes 0..31, (c2, c3, c1, c2) in lanes
+// 32..63.  Against the A operand (b1, b1, b1, b2 | b2, b2, b3, b3) of sa's split the
+// MFMA sums every product b_i c_j except b3 c3 (below 2^-32 of sa*sb).  lhm: all
+// ones in lanes 32..63 (bitwise selects: a select on the lane half compiled to a
+// branch).
+__device__ __forceinline__ v4h split_sb(float sb, uint32_t lhm) {
     const uint32_t c1 = __float_as_uint(sb) & 0xFFFF0000u;
-    const uint32_t c2 = __float_as_uint(sb - __uint_as_float(c1));
-    const uint32_t pk = __builtin_amdgcn_perm(c2, c1, 0x07060302u);   // c1 in the low half, c2 high
-    return __builtin_bit_cast(v4h, make_uint2(pk, lh ? 0u : pk));
+    const float r1 = sb - __uint_as_float(c1);
+    const uint32_t c2 = __float_as_uint(r1) & 0xFFFF0000u;
+    const uint32_t c3 = __float_as_uint(r1 - __uint_as_float(c2)) & 0xFFFF0000u;
+    const uint32_t p12 = (c1 >> 16) | c2, p31 = (c3 >> 16) | c1, p23 = (c2 >> 16) | c3;
+    return __builtin_bit_cast(v4h, make_uint2((p23 & lhm) | (p12 & ~lhm), (p12 & lhm) | (p31 & ~lhm)));
 }
 
 constexpr int BM = 128;           // activation rows per tile
@@ -232,6 +239,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6);
     const int lr = lane & 31, lh = lane >> 5;
+    const uint32_t lhm = 0u - (uint32_t)lh;   // all ones in lanes 32..63
     const int NG = K >> 7;
     const int P = gridDim.x;
     const int b = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
@@ -273,11 +281,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     };
     // Scale products of row tile ii on the matrix core: v_mfma_f32_32x32x8_bf16 (lane
     // l supplies row / column l & 31 at k = 4(l >> 5) .. +3) with
-    //   A: lanes 0..31 (b1, b1, b2, b2), lanes 32..63 (b3, b3, 0, 0)  of sa's split,
-    //   B: lanes 0..31 (c1, c2, c1, c2), lanes 32..63 (c1, c2, 0, 0)  of sb's split,
-    // gives S[r] = sum_ij b_i c_j = sa[row of register r] * sb[this lane's column] in
-    // the accumulator layout of the int8 tiles.  A row's split record holds the two
-    // dword pairs in that order, so lane (lr, lh) reads its pair at 8 * lh.
+    //   A: lanes 0..31 (b1, b1, b1, b2), lanes 32..63 (b2, b2, b3, b3)  of sa's split,
+    //   B: lanes 0..31 (c1, c2, c3, c1), lanes 32..63 (c2, c3, c1, c2)  of sb's split,
+    // gives S[r] = sum of b_i c_j over (i, j) != (3, 3) = sa[row of register r] *
+    // sb[this lane's column] in the accumulator layout of the int8 tiles.  A row's
+    // split record holds the two dword pairs in that order, so lane (lr, lh) reads
+    // its pair at 8 * lh.
     auto sa_of = [&](int ii) __attribute__((always_inline)) -> v4h {
         return *reinterpret_cast<const v4h*>(lds + rsa + ii * 512);
     };
@@ -545,7 +554,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // row tile 0, with the unpack of this unit's weights and the fold of the
         // previous unit's last tile
         read_a(a_nxt, 1);
-        const v4h sbz = split_sb(sbr, lh);
+        const v4h sbz = split_sb(sbr, lhm);
         // The scale products of each row tile are formed before its MFMAs, in the
         // buffer of its parity (even tiles Se, odd So), so they are ready long
         // before the tile is folded during the next row tile (configs[2]: ~1-2%

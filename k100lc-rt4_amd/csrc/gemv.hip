@@ -85,12 +85,10 @@ __device__ __forceinline__ uint4 pull_u4(uint4 v) {
 // 128-group, quarter q held by lanes j, j+16, j+32, j+48 -- as quant_act_a8_k
 // does: s = amax > 0 ? amax/127 : 1, c = clamp(rint(v/s), -128, 127).  Outputs the
 // interleaved bytes (per 8 elements [c0 c2 c4 c6 c1 c3 c5 c7]) as two dwordx4 and
-// the scale.  v/s uses a correctly rounded reciprocal y = 1/s and one
-// Markstein correction, t = RN(v*y), q = RN(t + RN(v - t*s)*y) with the residual
-// exact by FMA: for y = RN(1/s) and no underflow this is the correctly rounded
-// quotient (Markstein's theorem), i.e. bit-equal to v/s.  Scales outside
-// [2^-96, 2^100] (tiny or non-finite groups, where the residual could underflow)
-// take the IEEE division instead.
+// the scale.  v/s uses rt4_dev.h's div_by_recip (a correctly rounded reciprocal
+// and one fused correction step; equal to the IEEE quotient on every targeted
+// input checked, see there).  Scales outside [2^-96, 2^100] (tiny or non-finite
+// groups, where the residual could underflow) take the IEEE division instead.
 __device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
     const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c1, (uint32_t)c0, 0x0c0c0400u);
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c3, (uint32_t)c2, 0x0c0c0400u);

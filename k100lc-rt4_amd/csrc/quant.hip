@@ -41,11 +41,10 @@ __device__ __forceinline__ uint2 interleave8(const int c[8]) {
 // Outputs: xq int8 [rows][K] interleaved, sa f32 [rows][K/128], and optionally
 // asu = Σq per group (the reference needs it for its u=code+8 correction; the
 // MFMA GEMV here does not, but it is kept for parity checks).
-// x/s: for a wave whose scales all lie in [2^-96, 2^100], a correctly rounded
-// reciprocal y = 1/s and one Markstein correction, t = RN(x*y),
-// q = RN(t + RN(x - t*s)*y) with the residual exact by FMA, which for y = RN(1/s)
-// and no underflow is the correctly rounded quotient (Markstein's theorem), i.e.
-// bit-equal to x/s; other waves (tiny or non-finite groups) divide.
+// x/s: for a wave whose scales all lie in [2^-96, 2^100], rt4_dev.h's
+// div_by_recip (a correctly rounded reciprocal y = 1/s and one fused correction
+// step, equal to the IEEE quotient on every targeted input checked, see there);
+// other waves (tiny or non-finite groups) divide.
 // ALIGNED: x rows 16-byte aligned (vector loads); SUMS: asu is written.
 // grid (ceil(K/8/256), rows), block 256.
 template <bool ALIGNED, bool SUMS>

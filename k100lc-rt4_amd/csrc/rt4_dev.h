@@ -51,12 +51,18 @@ __device__ __forceinline__ uint32_t odd_x16(uint32_t w) { return w & 0xF0F0F0F0u
 // Saturating helpers for the quantizers (same clamp order as the reference).
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v > hi ? hi : (v < lo ? lo : v); }
 
-// x / s rounded to nearest through the reciprocal: with y = RN(1/s) (hipcc's
-// division is correctly rounded), t = RN(x*y) and the residual x - t*s exact by
-// FMA, RN(t + residual*y) is the correctly rounded quotient whenever nothing
-// underflows (Markstein's theorem), i.e. bit-equal to x / s.  The quantizers take
-// this path only when every scale of the wave lies in [2^-96, 2^100]; tiny or
-// non-finite scales divide.
+// x / s rounded to nearest through the reciprocal: y = RN(1/s) (hipcc's division
+// is correctly rounded), t = RN(x*y), then one correction RN(t + RN(x - t*s)*y)
+// with both steps fused.  Markstein's theorem gives RN(x/s) when t is faithful,
+// and t is not faithful everywhere (x/s just below a power of two can put it more
+// than one ulp away), so the equality with the IEEE quotient is not proven here.
+// It is checked on exact CPU emulations of this sequence at the inputs where it
+// could fail -- quotients within 8 ulp of every half-integer of the code range and
+// of powers of two, all-ones significands, the quantizers' own distributions, and
+// such a non-faithful t (tests/test_recip_div.py) -- and on the GPU against the
+// reference's quantizer kernels, which divide.  The quantizers take this path
+// only when every scale of the wave lies in [2^-96, 2^100]; tiny or non-finite
+// scales divide.
 __device__ __forceinline__ bool recip_div_ok(float s) { return s >= 0x1p-96f && s <= 0x1p+100f; }
 __device__ __forceinline__ float div_by_recip(float x, float s, float y) {
     const float t = x * y;
@@ -78,16 +84,17 @@ __device__ __forceinline__ float load_dev(const float* p) {
 
 // An fp32 activation scale split into three bf16 values b1 + b2 + b3 = s (each the
 // bf16 truncation of what is left, so both subtractions are exact and fp32's 24
-// significant bits fit in 3 x 8), packed as the prefill GEMM's scale-MFMA A operand:
-// {b1:b1, b2:b2, b3:b3, 0} as bf16 pairs.  Exact for every finite s at or above
-// 2^-110 (below that the last part can fall into fp32's subnormal range); an
-// infinite s gives NaN parts.
+// significant bits fit in 3 x 8), packed as the prefill GEMM's scale-MFMA A operand
+// (k = 0..3 in lanes 0..31, k = 4..7 in lanes 32..63): {b1:b1, b1:b2 | b2:b2, b3:b3}
+// as bf16 pairs (low half first).  Exact for every finite s at or above 2^-110
+// (below that the last part can fall into fp32's subnormal range); an infinite s
+// gives NaN parts.
 __device__ __forceinline__ uint4 split_scale_bf16x3(float s) {
     const uint32_t b1 = __float_as_uint(s) & 0xFFFF0000u;
     const float r1 = s - __uint_as_float(b1);
     const uint32_t b2 = __float_as_uint(r1) & 0xFFFF0000u;
     const uint32_t b3 = __float_as_uint(r1 - __uint_as_float(b2)) & 0xFFFF0000u;
-    return make_uint4(b1 | (b1 >> 16), b2 | (b2 >> 16), b3 | (b3 >> 16), 0u);
+    return make_uint4(b1 | (b1 >> 16), b2 | (b1 >> 16), b2 | (b2 >> 16), b3 | (b3 >> 16));
 }
 
 }  // namespace rt4

@@ -266,6 +266,33 @@ def gpu_cache(rt4, torch, q, k, v, TP, kv_cap, steps=None):
     return qq, qs, kc, ksc, vc, vsc, stage
 
 
+def test_tile_offsets_at_the_largest_cache_stay_in_range():
+    """The prefill kernel addresses one KV head's cache with 32-bit buffer offsets: per
+    tile t a scalar offset t * 64 keys * 128 bytes (K codes) and t * 8 * 256 * 4 bytes
+    (V codes), formed in unsigned 32-bit arithmetic, and prefetches up to three tiles
+    past the last.  At the largest cache the C ABI accepts, every such offset must not
+    wrap (so the buffer's range check sees it beyond the resource and returns the
+    zero codes), and the in-range ones must address the whole cache."""
+    import re
+    from conftest import PKG_DIR
+    src = (PKG_DIR / "csrc" / "attn.hip").read_text()
+    capi = (PKG_DIR / "csrc" / "capi.hip").read_text()
+    const = {k: int(re.search(rf"constexpr int {k} = (\d+);", src).group(1)) for k in ("HD", "BNK")}
+    HD, BNK = const["HD"], const["BNK"]
+    KDW = HD // 8
+    m = re.search(r"constexpr int kMaxKvCap = \(1 << (\d+)\) - (\d+);", capi)
+    cap = (1 << int(m.group(1))) - int(m.group(2))
+    n_tile = cap // BNK
+    for t in range(n_tile - 2, n_tile + 3):          # the last tiles and the prefetch beyond
+        sk = (t * BNK * KDW * 4) % 2 ** 32             # uint32 product, as the kernel forms it
+        sv = (t * (BNK // 8) * HD * 4) % 2 ** 32
+        assert sk == t * BNK * KDW * 4 and sv == t * (BNK // 8) * HD * 4, "offset wraps"
+        k_bytes, v_bytes = cap * KDW * 4, (cap // 8) * HD * 4   # resource sizes at n_kv = cap
+        assert (sk + 31 * 16 < k_bytes) == (t < n_tile) and (sv < v_bytes) == (t < n_tile)
+    # the K offset of the farthest prefetched tile is at least 2^31: beyond int, hence uint32
+    assert (n_tile + 2) * BNK * KDW * 4 >= 2 ** 31
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("T,n_kv,H,KVH,steps", [(48, 200, 3, 1, [(0, 37), (37, 100), (100, 200)]),
                                                 (64, 1024, 24, 4, [(0, 1024)]),

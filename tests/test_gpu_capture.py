@@ -132,6 +132,7 @@ CHILD = textwrap.dedent(r"""
     rt4_amd.release_scratch()
     rt4_amd.release_scratch()   # nothing left to free: still fine
     print("release: re-allocated scratch gives bit-identical GEMM, GEMV and attention", flush=True)
+
     print("CAPTURE-OK", flush=True)
 """)
 

@@ -191,3 +191,32 @@ def test_gemm_scale_products_over_wide_exponent_range(rt4, orc, torch_gpu):
     worst = max(rel_l2(y8[m], ref[m]) for m in range(M))
     print(f"  worst per-row rel_l2 = {worst:.3e}")
     assert worst < TIGHT
+
+
+def test_gemm_full_precision_fp32_weight_scales(rt4, orc, torch_gpu):
+    """wsc_gm holding arbitrary fp32 values (24 significant bits, not the fp16 values
+    make_group_major produces) over a wide exponent range: the scale products are
+    formed from three bf16 parts of each scale, so every row matches the fp64 oracle
+    to fp32 accuracy, for the int8 and the drop-in digit-plane entries alike."""
+    M, N, K = 256, 320, 1024
+    print(f"case gemm fp32 weight scales M={M} N={N} K={K}", flush=True)
+    c = workload.gemm_case(43, M, N, K)
+    rng = np.random.default_rng(43)
+    G = K // 128
+    sb_h = (rng.uniform(1, 2, (G, N)) * np.exp2(rng.integers(-30, 31, (G, N)))).astype(np.float32)
+    assert np.any(sb_h.astype(np.float16).astype(np.float32) != sb_h)   # not fp16-representable
+    wq, x = dev(torch_gpu, c["wq"]), dev(torch_gpu, c["x"])
+    sb = dev(torch_gpu, sb_h)
+    xq, sc8 = rt4.quant_rows_i8(x)
+    y8 = host(rt4.gemm_w4a8_i8(wq, sb, xq, sc8))
+    qh, ql, sc, sc16 = rt4.quant_rows_a8(x)
+    y = host(rt4.gemm_w4a8(wq, sb, qh, ql, sc, sc16))
+    assert np.array_equal(y.view(np.uint32), y8.view(np.uint32)), "digit-plane and int8 entries differ"
+    qh_o, ql_o, sc_o, sc16_o = orc.quant_rows_a8(c["x"], M, K)
+    mi = np.repeat(np.arange(M), N).astype(np.int32)
+    ni = np.tile(np.arange(N), M).astype(np.int32)
+    ref, _ = orc.gemm_w4a8_points(c["wq"], sb_h, qh_o, ql_o, sc_o, sc16_o, M, N, K, mi, ni)
+    ref = ref.reshape(M, N)
+    worst = max(rel_l2(y8[m], ref[m]) for m in range(M))
+    print(f"  worst per-row rel_l2 = {worst:.3e}")
+    assert worst < TIGHT
