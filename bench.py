@@ -56,6 +56,19 @@ def gemv_kernel_bytes(M: int, N: int, K: int) -> int:
     return N * K // 2 + N * NG * 2 + M * K + M * NG * 4 + M * N * 4
 
 
+# --only keys: (kernel, shape) pairs launched alone for per-shape profiler rows
+ONLY = {
+    "gemm_c2_gate_up": "int8 GEMM, M=1024 N=17408 K=5120",
+    "gemm_c2_down": "int8 GEMM, M=1024 N=5120 K=17408",
+    "gemm_ref_m2048": "int8 GEMM, M=2048 N=17408 K=5120",
+    "gemm_dropin_c2_gate_up": "drop-in digit-plane GEMM entry, M=1024 N=17408 K=5120",
+    "attn_c4": "FlashAttention prefill, 1024 queries over 32768 cached tokens",
+    "attn_ref_131k": "FlashAttention prefill, 1024 queries over 131072 cached tokens",
+    "gemv_gate_up_m4": "GEMV on quantized activations, M=4 N=17408 K=5120, 16 weight sets",
+    "gemv_c0_m1": "GEMV on quantized activations, M=1 N=5120 K=5120, 16 weight sets",
+}
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -71,6 +84,9 @@ def parse():
     ap.add_argument("--pmc-probe", action="store_true",
                     help="only launch the dominant kernels (gate/up GEMV, gate/up GEMM, C4 attention) and a "
                          "calibration copy, eagerly (for rocprofv3 --pmc)")
+    ap.add_argument("--only", choices=sorted(ONLY), default=None,
+                    help="only launch one kernel at one shape, eagerly, --steps times after 2 warm calls, and "
+                         "print its mean time (one rocprofv3 row per shape)")
     return ap.parse_args()
 
 
@@ -217,46 +233,61 @@ def cpu_baseline(step_bytes: int, seconds: float) -> dict:
             "blas": blas, **cpu_info(), "extra": out}
 
 
-def gemm_table(torch, rt4_amd, workload, gen) -> dict:
-    """Prefill GEMM: M=1024 tokens, gate/up and down shapes, as
-    int8-MFMA TOPS = 2*M*N*K / kernel time (GEMM launch only, graph-replayed), plus the
-    whole drop-in k_gemm_i4_a8 call (digit recombination + GEMM)."""
-    out = {}
-    for name, (M, N, K) in workload.GEMM_SHAPES.items():
-        wq, ws = workload.weights_torch(N, K, generator=gen)
-        sb = rt4_amd.make_group_major(ws, K)
+class GemmCase:
+    """Device operands of one prefill GEMM shape: random RT4 weights in group-major
+    scale order, outlier activations quantized for the int8 entry, the drop-in digit
+    planes and the W4A4 codes."""
+
+    def __init__(self, torch, rt4_amd, workload, gen, M, N, K):
+        self.M, self.N, self.K = M, N, K
+        self.wq, ws = workload.weights_torch(N, K, generator=gen)
+        self.sb = rt4_amd.make_group_major(ws, K)
         x = workload.acts_torch(M, K, outliers=True, generator=gen)
-        xq, sc = rt4_amd.quant_rows_i8(x)
-        qh, ql, sc_, sc16 = rt4_amd.quant_rows_a8(x)
-        c = torch.empty((M, N), device="cuda")
-        c2 = torch.empty((M, N), device="cuda")
-        reps = 10
-        aq4, sc4 = rt4_amd.quant_rows_a4(x)
+        self.xq, self.sc = rt4_amd.quant_rows_i8(x)
+        self.qh, self.ql, self.sc_, self.sc16 = rt4_amd.quant_rows_a8(x)
+        self.aq4, self.sc4 = rt4_amd.quant_rows_a4(x)
+        self.c = torch.empty((M, N), device="cuda")
+        self.c2 = torch.empty((M, N), device="cuda")
 
-        def gemm4():
-            for _ in range(reps):
-                rt4_amd.gemm_w4a4(wq, sb, aq4, sc4, out=c)
+    def int8(self, rt4_amd):
+        rt4_amd.gemm_w4a8_i8(self.wq, self.sb, self.xq, self.sc, out=self.c)
 
-        def gemm():
-            for _ in range(reps):
-                rt4_amd.gemm_w4a8_i8(wq, sb, xq, sc, out=c)
+    def dropin(self, rt4_amd):
+        rt4_amd.gemm_w4a8(self.wq, self.sb, self.qh, self.ql, self.sc_, self.sc16, out=self.c, c2=self.c2)
 
-        def dropin():
-            for _ in range(reps):
-                rt4_amd.gemm_w4a8(wq, sb, qh, ql, sc_, sc16, out=c, c2=c2)
+    def w4a4(self, rt4_amd):
+        rt4_amd.gemm_w4a4(self.wq, self.sb, self.aq4, self.sc4, out=self.c)
 
-        rt4_amd.gemm_w4a8_i8(wq, sb, xq, sc, out=c)           # eager first calls: kernel attributes
-        rt4_amd.gemm_w4a8(wq, sb, qh, ql, sc_, sc16, out=c, c2=c2)
-        rt4_amd.gemm_w4a4(wq, sb, aq4, sc4, out=c)
-        torch.cuda.synchronize()
-        us = timed_graph(torch, gemm) * 1e3 / reps
-        us_d = timed_graph(torch, dropin) * 1e3 / reps
-        us_4 = timed_graph(torch, gemm4) * 1e3 / reps
-        ops = 2 * M * N * K
-        out[f"gemm_{name}"] = {"us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
-                               "frac_i8_peak": round(ops / us / 1e6 / I8_PEAK_TOPS, 4),
-                               "dropin_us": round(us_d, 2), "w4a4_dropin_us": round(us_4, 2)}
-        del wq, ws, sb, x, xq, sc, qh, ql, sc_, sc16, c, c2, aq4, sc4
+
+def gemm_entry(torch, rt4_amd, g: GemmCase, w4a4: bool = True) -> dict:
+    """int8-MFMA TOPS = 2*M*N*K / kernel time (GEMM launch only, graph-replayed), plus
+    the whole drop-in k_gemm_i4_a8 call (digit recombination + GEMM)."""
+    reps = 10
+    runs = [("us", g.int8), ("dropin_us", g.dropin)] + ([("w4a4_dropin_us", g.w4a4)] if w4a4 else [])
+    for _, f in runs:                                          # eager first calls: kernel attributes
+        f(rt4_amd)
+    torch.cuda.synchronize()
+    res = {}
+    for key, f in runs:
+        res[key] = round(timed_graph(torch, lambda: [f(rt4_amd) for _ in range(reps)]) * 1e3 / reps, 2)
+    ops = 2 * g.M * g.N * g.K
+    res["TOPS"] = round(ops / res["us"] / 1e6, 1)
+    res["frac_i8_peak"] = round(ops / res["us"] / 1e6 / I8_PEAK_TOPS, 4)
+    return res
+
+
+def gemm_table(torch, rt4_amd, workload, gen) -> dict:
+    """Prefill GEMM: BASELINE configs[2] (M=1024 tokens, gate/up and down shapes) and
+    the reference's own benchmark shape (M=2048 tokens, gate/up)."""
+    out = {}
+    shapes = [(f"gemm_{n}", s, True) for n, s in workload.GEMM_SHAPES.items()]
+    shapes.append(("gemm_ref_m2048", workload.GEMM_REF_SHAPE, False))
+    for key, (M, N, K), w4a4 in shapes:
+        g = GemmCase(torch, rt4_amd, workload, gen, M, N, K)
+        out[key] = gemm_entry(torch, rt4_amd, g, w4a4)
+        if key == "gemm_ref_m2048":
+            out[key]["shape"] = [M, N, K]
+        del g
         torch.cuda.empty_cache()
     return out
 
@@ -290,48 +321,74 @@ def rt4_layers(rt4_amd, manifest: str, max_layers: int):
     return layers, shapes[0], shapes[1]
 
 
+class AttnCase:
+    """A filled int4 KV cache and quantized queries for one attention shape: n_q new
+    queries at positions ctx..ctx+n_q-1 over n_kv = ctx + n_q cached tokens."""
+
+    def __init__(self, torch, rt4_amd, workload, gen, cfg):
+        n_q, ctx, H, KVH, D = cfg["n_q"], cfg["ctx"], cfg["H"], cfg["KVH"], cfg["D"]
+        self.n_q, self.ctx, self.H, self.D, self.ratio = n_q, ctx, H, D, H // KVH
+        self.n_kv = n_kv = ctx + n_q
+        self.q, k, v = workload.attn_torch(n_q, n_kv, H, KVH, D, generator=gen)
+        self.qq, self.qs = rt4_amd.attn_q_quant(self.q, n_q)
+        self.kc = torch.zeros((KVH, n_kv, D // 8), dtype=torch.int32, device="cuda")
+        self.ksc = torch.ones((KVH, D // 128, n_kv), device="cuda")
+        self.vc = torch.zeros((KVH, n_kv // 8, D), dtype=torch.int32, device="cuda")
+        self.vsc = torch.ones((KVH, n_kv // 64, D), device="cuda")
+        self.stage = torch.zeros((KVH, 64, D), device="cuda")
+        rt4_amd.kv_append_k(self.kc, self.ksc, k, 0)
+        rt4_amd.kv_append_v(self.vc, self.vsc, self.stage, v, 0)
+        self.k_new, self.v_new = k[ctx:].contiguous(), v[ctx:].contiguous()
+        del k, v
+        self.out = None
+
+    def fa(self, rt4_amd):
+        self.out = rt4_amd.attention_prefill(self.qq, self.qs, self.kc, self.ksc, self.vc, self.vsc, n_kv=self.n_kv,
+                                             off=self.ctx, ratio=self.ratio, out=self.out)
+
+    def feed(self, rt4_amd):
+        rt4_amd.attn_q_quant(self.q, self.n_q, qq=self.qq, qs=self.qs)
+        rt4_amd.kv_append_k(self.kc, self.ksc, self.k_new, self.ctx)
+        rt4_amd.kv_append_v(self.vc, self.vsc, self.stage, self.v_new, self.ctx)
+
+    def ops(self) -> int:
+        """Two contractions of 2*D operations per visible (query, key) pair per head."""
+        return sum(self.ctx + i + 1 for i in range(self.n_q)) * 2 * 2 * self.D * self.H
+
+
 def attn_table(torch, rt4_amd, workload, gen) -> dict:
-    """int4-KV FlashAttention prefill: 24 query heads over 4 KV
-    heads, head dim 256, 1024 new queries over a 32768-token cache, causal.  Effective
-    int8-MFMA TOPS counts the two contractions over the keys each query sees
-    (2 * 2 * D per visible (query, key) pair per head); plus the Q quantizer and the
-    K/V cache append of the 1024 new tokens."""
-    c4 = workload.ATTN_C4
-    n_q, ctx, H, KVH, D = c4["n_q"], c4["ctx"], c4["H"], c4["KVH"], c4["D"]
-    n_kv = ctx + n_q
-    q, k, v = workload.attn_torch(n_q, n_kv, H, KVH, D, generator=gen)
-    qq, qs = rt4_amd.attn_q_quant(q, n_q)
-    kc = torch.zeros((KVH, n_kv, D // 8), dtype=torch.int32, device="cuda")
-    ksc = torch.ones((KVH, 2, n_kv), device="cuda")
-    vc = torch.zeros((KVH, n_kv // 8, D), dtype=torch.int32, device="cuda")
-    vsc = torch.ones((KVH, n_kv // 64, D), device="cuda")
-    stage = torch.zeros((KVH, 64, D), device="cuda")
-    rt4_amd.kv_append_k(kc, ksc, k, 0)
-    rt4_amd.kv_append_v(vc, vsc, stage, v, 0)
-    out = rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH)
-    torch.cuda.synchronize()
-    reps = 3
-
-    def fa():
-        for _ in range(reps):
-            rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH, out=out)
-
-    us = timed_graph(torch, fa) * 1e3 / reps
-    ops = sum(ctx + i + 1 for i in range(n_q)) * 2 * 2 * D * H
-    k_new, v_new = k[ctx:].contiguous(), v[ctx:].contiguous()
-
-    def feed():
-        rt4_amd.attn_q_quant(q, n_q, qq=qq, qs=qs)
-        rt4_amd.kv_append_k(kc, ksc, k_new, ctx)
-        rt4_amd.kv_append_v(vc, vsc, stage, v_new, ctx)
-
-    feed_us = timed_graph(torch, feed) * 1e3
-    res = {"attn_c4_prefill": {"us": round(us, 1), "TOPS_effective": round(ops / us / 1e6, 1),
-                               "frac_i8_peak": round(ops / us / 1e6 / I8_PEAK_TOPS, 4),
-                               "feeders_us": round(feed_us, 2)}}
-    del q, k, v, qq, qs, kc, ksc, vc, vsc, stage, out, k_new, v_new
-    torch.cuda.empty_cache()
+    """int4-KV FlashAttention prefill, 24 query heads over 4 KV heads, head dim 256,
+    causal: BASELINE configs[4] (1024 new queries over a 32768-token cache) and the
+    reference's own benchmark shape (over 131072 cached tokens).  Effective int8-MFMA
+    TOPS counts the two contractions over the keys each query sees; at C4 also the Q
+    quantizer and the K/V cache append of the 1024 new tokens."""
+    res = {}
+    for key, cfg, reps in (("attn_c4_prefill", workload.ATTN_C4, 3), ("attn_ref_131k_prefill", workload.ATTN_REF, 1)):
+        a = AttnCase(torch, rt4_amd, workload, gen, cfg)
+        a.fa(rt4_amd)
+        torch.cuda.synchronize()
+        us = timed_graph(torch, lambda: [a.fa(rt4_amd) for _ in range(reps)]) * 1e3 / reps
+        ops = a.ops()
+        res[key] = {"us": round(us, 1), "TOPS_effective": round(ops / us / 1e6, 1),
+                    "frac_i8_peak": round(ops / us / 1e6 / I8_PEAK_TOPS, 4)}
+        if key == "attn_c4_prefill":
+            res[key]["feeders_us"] = round(timed_graph(torch, lambda: a.feed(rt4_amd)) * 1e3, 2)
+        else:
+            res[key]["n_q_ctx"] = [a.n_q, a.ctx]
+        del a
+        torch.cuda.empty_cache()
     return res
+
+
+def pattern_entry(pat: dict, nbytes: int, kernel_us: float) -> dict:
+    """The GEMV's own memory requests without its compute (rt4p_gemv_loads): time per
+    launch, the rate at which it moves the GEMV's algorithmic bytes, and the GEMV's
+    time over it (the share of the GEMV that its load pattern accounts for)."""
+    return {"us": pat["us"], "GBs": round(nbytes / pat["us"] / 1e3, 1),
+            "frac": round(pat["us"] / kernel_us, 4),
+            "probe": f"rt4p_gemv_loads: the GEMV's grid and load form ({pat['groups_per_wave']} groups/wave, "
+                     f"{pat['waves']} waves, {pat['k_splits']} K pieces per leftover tile), weight/scale/activation "
+                     f"loads only, same weight sets back to back in a graph"}
 
 
 def load_traffic(key: str):
@@ -360,30 +417,14 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
         for wq, ws in mats:
             rt4_amd.gemv_w4a8_q(wq, ws, xq, sa, out=y)
     del mats
-    Mg, Ng, Kg = workload.GEMM_SHAPES["c2_gate_up"]
-    wq, ws = workload.weights_torch(Ng, Kg, generator=gen)
-    sb = rt4_amd.make_group_major(ws, Kg)
-    xg = workload.acts_torch(Mg, Kg, outliers=True, generator=gen)
-    xq8, sc = rt4_amd.quant_rows_i8(xg)
-    c = torch.empty((Mg, Ng), device="cuda")
+    g = GemmCase(torch, rt4_amd, workload, gen, *workload.GEMM_SHAPES["c2_gate_up"])
     for _ in range(3):
-        rt4_amd.gemm_w4a8_i8(wq, sb, xq8, sc, out=c)
-    del wq, ws, sb, xg, xq8, sc, c
-    c4 = workload.ATTN_C4
-    n_q, ctx, H, KVH, D = c4["n_q"], c4["ctx"], c4["H"], c4["KVH"], c4["D"]
-    n_kv = ctx + n_q
-    q, k, v = workload.attn_torch(n_q, n_kv, H, KVH, D, generator=gen)
-    qq, qs = rt4_amd.attn_q_quant(q, n_q)
-    kc = torch.zeros((KVH, n_kv, D // 8), dtype=torch.int32, device="cuda")
-    ksc = torch.ones((KVH, 2, n_kv), device="cuda")
-    vc = torch.zeros((KVH, n_kv // 8, D), dtype=torch.int32, device="cuda")
-    vsc = torch.ones((KVH, n_kv // 64, D), device="cuda")
-    stage = torch.zeros((KVH, 64, D), device="cuda")
-    rt4_amd.kv_append_k(kc, ksc, k, 0)
-    rt4_amd.kv_append_v(vc, vsc, stage, v, 0)
+        g.int8(rt4_amd)
+    del g
+    a = AttnCase(torch, rt4_amd, workload, gen, workload.ATTN_C4)
     for _ in range(3):
-        rt4_amd.attention_prefill(qq, qs, kc, ksc, vc, vsc, n_kv=n_kv, off=ctx, ratio=H // KVH)
-    del q, k, v, qq, qs, kc, ksc, vc, vsc, stage
+        a.fa(rt4_amd)
+    del a
     nb = profiling.COPY_BYTES
     src = torch.empty(nb // 4, dtype=torch.int32, device="cuda").random_()
     dst = torch.empty_like(src)
@@ -395,6 +436,39 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
             raise RuntimeError(f"rt4p_copy failed ({rc})")
     torch.cuda.synchronize()
     print("pmc probe done", flush=True)
+    return 0
+
+
+def only_one(torch, rt4_amd, workload, gen, key: str, launches: int) -> int:
+    """Eager launches of one kernel at one shape (--only): 2 warm calls, then
+    `launches` calls timed together with events; prints one JSON line."""
+    if key.startswith("gemm_"):
+        shape = {"gemm_c2_gate_up": workload.GEMM_SHAPES["c2_gate_up"], "gemm_c2_down": workload.GEMM_SHAPES["c2_down"],
+                 "gemm_ref_m2048": workload.GEMM_REF_SHAPE,
+                 "gemm_dropin_c2_gate_up": workload.GEMM_SHAPES["c2_gate_up"]}[key]
+        c = GemmCase(torch, rt4_amd, workload, gen, *shape)
+        fn = (lambda: c.dropin(rt4_amd)) if "dropin" in key else (lambda: c.int8(rt4_amd))
+    elif key.startswith("attn_"):
+        c = AttnCase(torch, rt4_amd, workload, gen, workload.ATTN_C4 if key == "attn_c4" else workload.ATTN_REF)
+        fn = lambda: c.fa(rt4_amd)  # noqa: E731
+    else:
+        M, N, K = (4, 17408, 5120) if key == "gemv_gate_up_m4" else (1, 5120, 5120)
+        mats = [workload.weights_torch(N, K, generator=gen) for _ in range(16)]
+        xq, sa = rt4_amd.quant_act_a8(workload.acts_torch(M, K, generator=gen))
+        y = torch.empty((M, N), device="cuda")
+        it = iter(range(1 << 62))
+        fn = lambda: rt4_amd.gemv_w4a8_q(*mats[next(it) % 16], xq, sa, out=y)  # noqa: E731
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(launches):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"only": key, "what": ONLY[key], "launches": launches,
+                      "us_per_launch_eager": round(t0.elapsed_time(t1) * 1e3 / launches, 2)}), flush=True)
     return 0
 
 
@@ -416,6 +490,8 @@ def main() -> int:
     gen = torch.Generator(device="cuda").manual_seed(0)
     if args.pmc_probe:
         return pmc_probe(torch, rt4_amd, workload, gen)
+    if args.only:
+        return only_one(torch, rt4_amd, workload, gen, args.only, max(1, args.steps))
     M = 4
     (Ngu, Kgu), (Nd, Kd) = (17408, 5120), (5120, 17408)
     L = max(1, args.layers)
@@ -486,18 +562,20 @@ def main() -> int:
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     plan = rt4_amd.gemv_launch_plan(M, Ngu, Kgu)
     g_, w_, rb_ = plan["groups_per_wave"], plan["waves"], plan["row_blocks"]
-    # line-wise activation loads: one row block and their LDS slices within 64 KB (the launcher's rule)
-    al = rb_ == 1 and w_ * 16 * g_ * 2 + w_ * M * 16 * 4 + w_ * M * g_ * 8 * 16 <= 65536
-    # scales hoisted out of the chunk loop: 2 groups per wave, even K/128, 3-8 chunks per wave, <= 4 waves
-    ng_gu = Kgu // 128
-    per_wave = -(-(-(-ng_gu // g_)) // w_)
-    hs = al and g_ == 2 and ng_gu % 2 == 0 and w_ <= 4 and 3 <= per_wave <= 8
+    if g_ == 4 and rb_ == 1 and Kgu % 512 == 0 and w_ <= 8:
+        kname = f"rt4::gemv_w4a8_tl_k<{M},false>"        # the row-transposed form
+    else:
+        # line-wise activation loads: one row block and their LDS slices within 64 KB (the launcher's rule)
+        al = rb_ == 1 and w_ * 16 * g_ * 2 + w_ * M * 16 * 4 + w_ * M * g_ * 8 * 16 <= 65536
+        # scales hoisted out of the chunk loop: 2 groups per wave, even K/128, 3-8 chunks per wave, <= 4 waves
+        ng_gu = Kgu // 128
+        per_wave = -(-(-(-ng_gu // g_)) // w_)
+        hs = al and g_ == 2 and ng_gu % 2 == 0 and w_ <= 4 and 3 <= per_wave <= 8
+        kname = f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false,{str(hs).lower()}>"
     # measured ceiling: the fastest single launch that reads the same byte count
     from rt4_amd import probe
     ceil_gu = probe.read_ceiling(torch, gu_bytes, timed_graph=timed_graph)
-    roofline = {"kernel": f"rt4::gemv_w4a8_k<{M},{g_},{rb_},{str(al).lower()},false,false,{str(hs).lower()}> "
-                          f"(gate/up GEMV, "
-                          f"M={M} K={Kgu} N={Ngu}, "
+    roofline = {"kernel": f"{kname} (gate/up GEMV, M={M} K={Kgu} N={Ngu}, {g_} groups/wave, "
                           f"{plan['waves']} waves/tile, {plan['k_splits']} K pieces/leftover tile)",
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("gemv_gate_up"),
@@ -508,6 +586,9 @@ def main() -> int:
                                   "probe": f"one-pass read of the same {gu_bytes} bytes (rt4p_read_burst, "
                                            f"{ceil_gu['blocks']}x{ceil_gu['threads']}, non-temporal), 16 buffers "
                                            f"back to back in a graph"}}
+    pat_gu = probe.gemv_load_pattern(torch, rt4_amd, gu_mats, xq_gu, M, timed_graph)
+    if pat_gu:
+        roofline["load_pattern"] = pattern_entry(pat_gu, gu_bytes, gu_us)
 
     kernels = {}
     if not args.no_extra:
@@ -534,6 +615,9 @@ def main() -> int:
         kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(d_bytes / d_us / 1e3, 1),
                                    "measured_peak_GBs": ceil_d["GBs"],
                                    "frac_measured": round(d_bytes / d_us / 1e3 / ceil_d["GBs"], 4)}
+        pat_d = probe.gemv_load_pattern(torch, rt4_amd, d_mats, xq_d, M, timed_graph)
+        if pat_d:
+            kernels["gemv_down_m4"]["load_pattern"] = pattern_entry(pat_d, d_bytes, d_us)
 
         def gemv_gu_fused():   # its own best measured config: 4 groups per wave, 8 waves
             for wq, ws in gu_mats:
@@ -563,8 +647,18 @@ def main() -> int:
         kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(c0_bytes / c0_us / 1e3, 1),
                                  "measured_peak_GBs": ceil_c0["GBs"], "measured_peak_us": ceil_c0["us"],
                                  "frac_measured": round(c0_bytes / c0_us / 1e3 / ceil_c0["GBs"], 4)}
+        pat_c0 = probe.gemv_load_pattern(torch, rt4_amd, c0_mats, xq1, 1, timed_graph)
+        if pat_c0:
+            kernels["gemv_c0_m1"]["load_pattern"] = pattern_entry(pat_c0, c0_bytes, c0_us)
         kernels["ceilings"] = {"mfma_i32_16x16x64_i8_TOPS": probe.mfma_i8_rate(torch),
                                "mfma_i32_32x32x32_i8_TOPS": probe.mfma_i8_rate(torch, big=True),
+                               **probe.mfma_f8f6f4_rates(torch),
+                               "gemm_unit_skeleton": probe.gemm_unit_cycles(torch),
+                               "graph_node_us": probe.launch_cost(torch, timed_graph),
+                               "gemv_load_pattern_us": {k: v["load_pattern"]["us"] for k, v in
+                                                        (("gemv_gate_up_m4", roofline), ("gemv_down_m4",
+                                                         kernels["gemv_down_m4"]), ("gemv_c0_m1", kernels["gemv_c0_m1"]))
+                                                        if "load_pattern" in v},
                                "published_i8_TOPS": I8_PEAK_TOPS, "published_hbm_GBs": HBM_PEAK_GBS}
         # LM head (C3): M=4, K=5120, N=248320, two 0.66 GB copies alternated
         del layers, gu_mats, d_mats, c0_mats
@@ -575,7 +669,9 @@ def main() -> int:
         # instruction each kernel runs (the GEMM 32x32x32, the attention 16x16x64)
         for key, rate in (("gemm_c2_gate_up", "mfma_i32_32x32x32_i8_TOPS"),
                           ("gemm_c2_down", "mfma_i32_32x32x32_i8_TOPS"),
-                          ("attn_c4_prefill", "mfma_i32_16x16x64_i8_TOPS")):
+                          ("gemm_ref_m2048", "mfma_i32_32x32x32_i8_TOPS"),
+                          ("attn_c4_prefill", "mfma_i32_16x16x64_i8_TOPS"),
+                          ("attn_ref_131k_prefill", "mfma_i32_16x16x64_i8_TOPS")):
             tops = kernels[key].get("TOPS", kernels[key].get("TOPS_effective"))
             kernels[key]["frac_measured_issue"] = round(tops / kernels["ceilings"][rate], 4)
         lm = [workload.weights_torch(248320, 5120, generator=gen) for _ in range(2)]

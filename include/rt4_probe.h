@@ -36,6 +36,23 @@ int rt4p_copy(void* dst, const void* src, size_t bytes, int blocks, void* stream
 int rt4p_mfma_i8(void* sink, int big, int iters, int blocks, void* stream);
 /* `iters` x 8 independent v_fma_f32 per lane. */
 int rt4p_valu_fma(void* sink, int iters, int blocks, void* stream);
+/* The decode GEMV's memory requests alone, for a launch plan (rt4_gemv_launch_plan)
+ * of one 16-row block, `groups_per_wave` 2 (8 rows x 128 B per weight load, up to
+ * 16 waves) or 4 (the row-transposed form, 4 rows x 256 B, up to 8 waves), `waves`
+ * waves and `k_splits` pieces per leftover tile: wq/ws/xq as rt4_gemv_w4a8_q takes
+ * them, `cus` the device's CU count.  rows 1..4, K a multiple of 128*groups_per_wave. */
+int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, void* sink, int rows, int N, int K,
+                    int groups_per_wave, int waves, int k_splits, int cus, void* stream);
+/* An empty kernel of `blocks` x `threads`. */
+int rt4p_empty(int blocks, int threads, void* stream);
+/* `iters` x 4 independent v_mfma_scale_f32_32x32x64_f8f6f4 per wave (65536 MACs
+ * each), 512 threads per block; fmt 0 FP8 E4M3, 2 FP6 E2M3, 4 FP4 E2M1 for both
+ * operands. */
+int rt4p_mfma_f8f6f4(void* sink, int fmt, int iters, int blocks, void* stream);
+/* `units` iterations of the prefill GEMM's per-unit instruction skeleton (registers
+ * only) per wave, 512 threads per block: variant 0 the int8 form, 1 the FP8-digit
+ * form (see probe.hip). */
+int rt4p_gemm_unit(void* sink, int variant, int units, int blocks, void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

@@ -134,6 +134,76 @@ __device__ __forceinline__ void quant_lane(const float4 (&x)[8], uint4& a0, uint
 template <int M, int GPW>
 constexpr int gemv_al_bytes() { return M * GPW * 8 * 16; }
 
+// The end of a tile, shared by the GEMV kernels: the W waves' partial sums are
+// reduced through LDS (`red`: W x RB*M*16 floats), in wave order, and written out;
+// a K range of a split tile instead publishes its partial (agent-coherent store),
+// counts itself in, and the last piece to arrive sums all pieces in order
+// (deterministic) and resets the counter for the next call.  No workgroup waits
+// for another.  Outputs of the tile: o = (rb*M + r)*16 + l is row r, column
+// n0 + 16 rb + l.
+template <int M, int RB>
+__device__ __forceinline__ void tile_finish(const float (&yacc)[RB][M], float* red, float* __restrict__ y, int N,
+                                            int n0, int W, int w, int lane, bool piece, int b, int rem,
+                                            const GemvSplit& sp) {
+    constexpr int NOUT = RB * M * 16;
+    if (W == 1 && !piece) {
+        if (lane < 16)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int r = 0; r < M; r++)
+                    if (n0 + 16 * rb + lane < N) y[(size_t)r * N + n0 + 16 * rb + lane] = yacc[rb][r];
+        return;
+    }
+    if (lane < 16)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int r = 0; r < M; r++) red[(w * NOUT) + (rb * M + r) * 16 + lane] = yacc[rb][r];
+    __syncthreads();
+    // each thread sums the waves' partials of outputs o = threadIdx.x + i*blockDim.x
+    constexpr int OPT = (NOUT + 63) / 64;    // outputs per thread at one wave (upper bound)
+    float tot[OPT];
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        tot[i] = 0.f;
+        if (o < NOUT)
+            for (int v = 0; v < W; v++) tot[i] += red[v * NOUT + o];
+    }
+    if (!piece) {
+#pragma unroll
+        for (int i = 0; i < OPT; i++) {
+            const int o = threadIdx.x + i * blockDim.x;
+            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
+            if (o < NOUT && n < N) y[(size_t)r * N + n] = tot[i];
+        }
+        return;
+    }
+    __shared__ int s_last;
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        if (o < NOUT) store_dev(sp.part + (size_t)b * NOUT + o, tot[i]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(sp.cnt + rem, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sp.S - 1;
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int i = 0; i < OPT; i++) {
+        const int o = threadIdx.x + i * blockDim.x;
+        if (o < NOUT) {
+            float sum = 0.f;
+            for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + (size_t)(rem * sp.S + v) * NOUT + o);
+            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
+            if (n < N) y[(size_t)r * N + n] = sum;
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + rem, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int M, int GPW, int RB, bool AL, bool GSUM, bool QIN, bool HS>
 __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__ wq,
                                                     const uint16_t* __restrict__ ws,
@@ -406,67 +476,171 @@ __global__ __launch_bounds__(1024) void gemv_w4a8_k(const uint32_t* __restrict__
         }
     }
 
-    // Outputs of the tile: o = (rb*M + r)*16 + l is row r, column n0 + 16 rb + l.
-    constexpr int NOUT = RB * M * 16;
-    if (W == 1 && !piece) {
-        if (lane < 16)
+    tile_finish<M, RB>(yacc, red, y, N, n0, W, w, lane, piece, b, rem, sp);
+}
+
+// ---- Row-transposed loads (TL): the configuration of gemv_w4a8_k with 4 groups
+// per wave, one 16-row block, line-wise activations and pre-quantized input, for
+// K a multiple of 512 and at most 8 waves.  Same chunk-to-wave assignment, same
+// group order within a wave and the same fold, so its outputs are bit-identical
+// to gemv_w4a8_k's on that configuration; only the weight stream differs.
+//
+// * A chunk (4 groups of 16 rows, 16 x 256 B) is read by four dwordx4 load
+//   instructions of 4 rows x 256 B each: instruction k, lane l reads row
+//   4k + l/16, 16-byte piece (l%16) ^ (4k + l/16) of the row's 256 B.  Longer runs
+//   per row than gemv_w4a8_k's 8 rows x 128 B measured ~8% faster for the load
+//   stream alone at the 27B shapes.
+// * A wave holds one chunk at a time: its scales, activations and weights are
+//   issued together (64 B of weights per lane, twice gemv_w4a8_k's two-group
+//   chunk), then used.  About 70 VGPRs, so ~7 waves per SIMD stay resident and
+//   other waves' loads cover a wave's arithmetic.  Holding 2 or 4 chunks per wave
+//   (all issued before the first is used) measured 5-15% slower: the extra
+//   registers cost more residency than the deeper queue gains.
+// * The MFMA operand needs row j in lanes j, j+16, j+32, j+48, so each chunk goes
+//   through a wave-private 4 KB LDS slice: written lane-linearly (conflict-free),
+//   read back as lane (j, q) <- row j, piece 4u + q for group u; the XOR of the
+//   piece index with the row keeps the 16 lanes of each read quarter on distinct
+//   banks.
+template <int M, bool GSUM>
+__device__ __forceinline__ void tl_chunk(const unsigned char* const (&pk)[4], const uint16_t* wsr,
+                                          const int8_t* __restrict__ xq, const float* __restrict__ sa,
+                                          int32_t* __restrict__ gsum, uint4* tl, uint4* axl, int c, int NG,
+                                          int K, int N, int n0, int lane, float (&yacc)[1][M]) {
+    constexpr int GPW = 4, GPS = 16 / M, NSET = (GPW + GPS - 1) / GPS;
+    constexpr int ACH = M * GPW * 8, AIN = (ACH + 63) / 64;
+    constexpr int RSH = M == 1 ? 3 : M == 2 ? 2 : 1;    // activation slice swizzle, as gemv_w4a8_k
+    const int j = lane & 15, q = lane >> 4;
+    const int jr = j % M, jg = j / M;
+    const v4i zero = {0, 0, 0, 0};
+    const int g0 = uniform(c * GPW);
+    // the chunk's scales, activations and weights, all issued before any wait (the
+    // scheduler would otherwise sink the later loads behind the first wait); the
+    // activations go first, so the LDS staging can start while weights arrive
+    uint32_t sw[2];
+    v4u araw[AIN], wv[4];
+    sw[0] = *reinterpret_cast<const uint32_t*>(wsr + g0);
+    sw[1] = *reinterpret_cast<const uint32_t*>(wsr + g0 + 2);
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-                for (int r = 0; r < M; r++)
-                    if (n0 + 16 * rb + lane < N) y[(size_t)r * N + n0 + 16 * rb + lane] = yacc[rb][r];
-        return;
+    for (int t = 0; t < AIN; t++) {
+        int e = t * 64 + lane;
+        e = e < ACH ? e : ACH - 1;
+        const int row = e / (GPW * 8), grp = (e / 8) % GPW, cc = e % 8;
+        araw[t] = *reinterpret_cast<const v4u*>(xq + (size_t)row * K + (size_t)(g0 + grp) * 128 + cc * 16);
     }
-    if (lane < 16)
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
+    for (int k = 0; k < 4; k++) wv[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(pk[k] + (size_t)g0 * 64));
+    __builtin_amdgcn_sched_barrier(0);
+    {
 #pragma unroll
-            for (int r = 0; r < M; r++) red[(w * NOUT) + (rb * M + r) * 16 + lane] = yacc[rb][r];
-    __syncthreads();
-    // each thread sums the waves' partials of outputs o = threadIdx.x + i*blockDim.x
-    constexpr int OPT = (NOUT + 63) / 64;    // outputs per thread at one wave (upper bound)
-    float tot[OPT];
+        for (int k = 0; k < 4; k++) tl[k * 64 + lane] = make_uint4(wv[k].x, wv[k].y, wv[k].z, wv[k].w);
 #pragma unroll
-    for (int i = 0; i < OPT; i++) {
-        const int o = threadIdx.x + i * blockDim.x;
-        tot[i] = 0.f;
-        if (o < NOUT)
-            for (int v = 0; v < W; v++) tot[i] += red[v * NOUT + o];
-    }
-    if (!piece) {
-#pragma unroll
-        for (int i = 0; i < OPT; i++) {
-            const int o = threadIdx.x + i * blockDim.x;
-            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
-            if (o < NOUT && n < N) y[(size_t)r * N + n] = tot[i];
+        for (int t = 0; t < AIN; t++) {
+            const int e = t * 64 + lane;
+            if (e < ACH) {
+                const int row = e / (GPW * 8), grp = (e / 8) % GPW, cc = e % 8;
+                const int h = ((row << RSH) + (grp >> 1)) & 7;
+                axl[(row * GPW + grp) * 8 + (cc ^ h)] = make_uint4(araw[t].x, araw[t].y, araw[t].z, araw[t].w);
+            }
         }
-        return;
-    }
-    // A K range of a split tile: publish the partial (agent-coherent store), count
-    // the pieces in, and let the last one sum all pieces in order (deterministic)
-    // and reset the counter for the next call.  No workgroup waits for another.
-    __shared__ int s_last;
+        // LDS operations of one wave complete in order, so no barrier is needed; the
+        // fences only keep the compiler's order
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        uint4 wt[4];
 #pragma unroll
-    for (int i = 0; i < OPT; i++) {
-        const int o = threadIdx.x + i * blockDim.x;
-        if (o < NOUT) store_dev(sp.part + (size_t)b * NOUT + o, tot[i]);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(sp.cnt + rem, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == sp.S - 1;
-    __syncthreads();
-    if (!s_last) return;
+        for (int u = 0; u < 4; u++) wt[u] = tl[j * 16 + ((4 * u + q) ^ j)];
+        uint4 ax0[NSET], ax1[NSET];
 #pragma unroll
-    for (int i = 0; i < OPT; i++) {
-        const int o = threadIdx.x + i * blockDim.x;
-        if (o < NOUT) {
-            float sum = 0.f;
-            for (int v = 0; v < sp.S; v++) sum += load_dev(sp.part + (size_t)(rem * sp.S + v) * NOUT + o);
-            const int n = n0 + 16 * (o / (M * 16)) + (o & 15), r = (o >> 4) % M;
-            if (n < N) y[(size_t)r * N + n] = sum;
+        for (int s = 0; s < NSET; s++) {
+            int grp = s * GPS + jg;
+            grp = grp < GPW ? grp : GPW - 1;          // lanes past the chunk: unused
+            const int h = ((jr << RSH) + (grp >> 1)) & 7;
+            ax0[s] = axl[(jr * GPW + grp) * 8 + ((2 * q) ^ h)];
+            ax1[s] = axl[(jr * GPW + grp) * 8 + ((2 * q + 1) ^ h)];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int g = g0 + u;
+            uint4 xa, xb;
+            switch (u % GPS) {
+#define RT4_PULL(I)                                      \
+    case I:                                              \
+        xa = pull_u4<((I) * M) & 15>(ax0[u / GPS]);      \
+        xb = pull_u4<((I) * M) & 15>(ax1[u / GPS]);      \
+        break;
+                RT4_PULL(0) RT4_PULL(1) RT4_PULL(2) RT4_PULL(3)
+#undef RT4_PULL
+            }
+            const v4i A0 = {(int)xa.x, (int)xa.y, (int)xa.z, (int)xa.w};
+            const v4i A1 = {(int)xb.x, (int)xb.y, (int)xb.z, (int)xb.w};
+            float a_s[M];
+#pragma unroll
+            for (int r = 0; r < M; r++) a_s[r] = sa[(size_t)r * NG + g];
+            const uint4 qv = wt[u];
+            const v4i b0 = {(int)even_x16(qv.x), (int)odd_x16(qv.x), (int)even_x16(qv.y), (int)odd_x16(qv.y)};
+            const v4i b1 = {(int)even_x16(qv.z), (int)odd_x16(qv.z), (int)even_x16(qv.w), (int)odd_x16(qv.w)};
+            v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, b0, zero, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, b1, acc, 0, 0, 0);
+            // lane l < 16 now holds 16*I[m=r][n0+l] in acc[r]
+            const int nl = n0 + lane;
+            if (GSUM && lane < 16 && nl < N)
+#pragma unroll
+                for (int r = 0; r < M; r++) gsum[((size_t)r * N + nl) * NG + g] = acc[r] >> 4;
+            const uint32_t pair = sw[u >> 1];
+            const float s16 = f16_bits_to_f32((uint16_t)((u & 1) ? pair >> 16 : pair & 0xFFFFu)) * 0.0625f;
+#pragma unroll
+            for (int r = 0; r < M; r++) yacc[0][r] = fmaf((float)acc[r], s16 * a_s[r], yacc[0][r]);
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + rem, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS bytes of a TL workgroup of W waves: transposition slices, activation slices,
+// reduction area.
+template <int M>
+constexpr size_t gemv_tl_lds(int W) {
+    return (size_t)W * 4096 + (size_t)W * gemv_al_bytes<M, 4>() + (size_t)W * M * 16 * sizeof(float);
+}
+
+template <int M, bool GSUM>
+__global__ __launch_bounds__(512) void gemv_w4a8_tl_k(const uint32_t* __restrict__ wq,
+                                                      const uint16_t* __restrict__ ws,
+                                                      const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ sa,
+                                                      float* __restrict__ y,
+                                                      int32_t* __restrict__ gsum, int N, int K, GemvSplit sp) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, w = uniform(threadIdx.x >> 6);
+    const int j = lane & 15;
+    const int NG = K >> 7, RS = K >> 1, NC = NG >> 2;
+    const int b = blockIdx.x, npieces = sp.nrem * sp.S;
+    const bool piece = b < npieces;
+    const int rem = piece ? b / sp.S : 0, pc = piece ? b % sp.S : 0;
+    const int tile = piece ? sp.full + rem : b - npieces;
+    const int c_lo = piece ? pc * NC / sp.S : 0, c_hi = piece ? (pc + 1) * NC / sp.S : NC;
+    const int n0 = tile * 16;
+    uint4* tl = reinterpret_cast<uint4*>(smem) + (size_t)w * 256;
+    uint4* axl = reinterpret_cast<uint4*>(smem + (size_t)W * 4096) + (size_t)w * (M * 4 * 8);
+    float* red = reinterpret_cast<float*>(smem + (size_t)W * 4096 + (size_t)W * gemv_al_bytes<M, 4>());
+    const unsigned char* pk[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int rho = 4 * k + (lane >> 4);
+        int r = n0 + rho;
+        r = r < N ? r : N - 1;                   // tail rows read a valid row; dropped
+        pk[k] = reinterpret_cast<const unsigned char*>(wq) + (size_t)r * RS + (((lane & 15) ^ rho) * 16);
+    }
+    const uint16_t* wsr = ws + (size_t)(n0 + j < N ? n0 + j : N - 1) * NG;
+    float yacc[1][M];
+#pragma unroll
+    for (int r = 0; r < M; r++) yacc[0][r] = 0.f;
+    for (int c = c_lo + w; c < c_hi; c += W)
+        tl_chunk<M, GSUM>(pk, wsr, xq, sa, gsum, tl, axl, c, NG, K, N, n0, lane, yacc);
+    tile_finish<M, 1>(yacc, red, y, N, n0, W, w, lane, piece, b, rem, sp);
 }
 
 template <int M, int GPW, int RB, bool GSUM, bool QIN>
@@ -478,6 +652,15 @@ hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_
     const int grid = sp.full + sp.nrem * sp.S;
     // line-wise activation loads where they apply and their LDS slices fit the
     // default 64 KB of dynamic LDS
+    if constexpr (RB == 1 && !QIN && GPW == 4) {
+        // row-transposed loads: same results, faster weight stream
+        const int NG = K / kGroup;
+        if (NG % 4 == 0 && waves <= 8 && gemv_tl_lds<M>(waves) <= 65536) {
+            hipLaunchKernelGGL((gemv_w4a8_tl_k<M, GSUM>), dim3(grid), dim3(64 * waves), gemv_tl_lds<M>(waves), st, wq,
+                               ws, xq, sa, y, gsum, N, K, sp);
+            return hipGetLastError();
+        }
+    }
     if constexpr (RB == 1 && !QIN) {
         if (base + al <= 65536) {
             // Scales hoisted out of the chunk loop where a wave has at least 3 and at
@@ -563,6 +746,19 @@ GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
     // 7.8, 17408 10.8 vs 10.9.  Beyond that (the LM head at 1-2 rows: 109 vs 97
     // us) the general rule wins.
     const double tpc = (double)ntiles / cus;
+    // Two to four rows with K a multiple of 512: 4 groups per wave, which runs the
+    // row-transposed kernel (gemv_w4a8_tl_k).  Measured on MI355X (us, this rule
+    // vs the 2-group rule below): M=4 K=5120 N=17408 10.5 vs 11.2, N=10240 7.7
+    // vs 8.1; K=17408 N=5120 10.9 vs 11.2, N=17408 31.8 vs 36.0; M=2 K=5120
+    // N=17408 10.2 vs 10.9.  One row gains nothing measurable (C0 6.0 either way).
+    if (c.rb == 1 && rows >= 2 && NG % 4 == 0 && (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
+        c.gpw = 4;
+        int w = tpc <= 2.75 ? 8 : rows == 3 ? 4 : 2;
+        const int nc = NG / 4;
+        c.waves = w < nc ? w : nc;
+        c.max_split = 4;
+        return c;
+    }
     if (c.rb == 1 && (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
         c.gpw = 2 < ng_even ? 2 : ng_even;
         const int nc = (NG + c.gpw - 1) / c.gpw;

@@ -6,7 +6,8 @@ import ctypes
 import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "librt4probe.so"
-EXPORTS = ("rt4p_hbm_read", "rt4p_read_burst", "rt4p_copy", "rt4p_mfma_i8", "rt4p_valu_fma")
+EXPORTS = ("rt4p_hbm_read", "rt4p_read_burst", "rt4p_copy", "rt4p_mfma_i8", "rt4p_valu_fma", "rt4p_gemv_loads",
+           "rt4p_empty", "rt4p_mfma_f8f6f4", "rt4p_gemm_unit")
 _lib = None
 
 
@@ -21,7 +22,9 @@ def lib() -> ctypes.CDLL:
         P, I, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
         sigs = {"rt4p_hbm_read": [P, Z, P, I, P], "rt4p_read_burst": [P, Z, P, I, I, I, P],
                 "rt4p_copy": [P, P, Z, I, P],
-                "rt4p_mfma_i8": [P, I, I, I, P], "rt4p_valu_fma": [P, I, I, P]}
+                "rt4p_mfma_i8": [P, I, I, I, P], "rt4p_valu_fma": [P, I, I, P],
+                "rt4p_gemv_loads": [P, P, P, P, I, I, I, I, I, I, I, P], "rt4p_empty": [I, I, P],
+                "rt4p_mfma_f8f6f4": [P, I, I, I, P], "rt4p_gemm_unit": [P, I, I, I, P]}
         for name, args in sigs.items():
             getattr(L, name).argtypes = args
             getattr(L, name).restype = ctypes.c_int
@@ -126,3 +129,87 @@ def mfma_i8_rate(torch, big: bool = False, iters: int = 2048) -> float:
     ms = _timed(torch, lambda: L.rt4p_mfma_i8(ctypes.c_void_p(sink.data_ptr()), 1 if big else 0, iters, blocks, st))
     macs = 32768 if big else 16384
     return round(2.0 * macs * 4 * iters * blocks * 4 / ms / 1e9, 1)
+
+
+def gemv_load_pattern(torch, rt4_amd, mats, xq, rows: int, timed_graph) -> dict | None:
+    """The decode GEMV's memory requests alone (rt4p_gemv_loads) over the weight sets
+    `mats` [(wq, ws)] with activations xq, back to back in a graph as the GEMV is
+    timed: {"us": per launch, "groups_per_wave", "waves", "k_splits"}.  None when the
+    shape's launch plan is not a one-row-block form the probe mirrors."""
+    wq0, _ = mats[0]
+    N, K = wq0.shape[0], wq0.shape[1] * 8
+    for wq, ws in mats:
+        if tuple(wq.shape) != (N, K // 8) or tuple(ws.shape) != (N, K // 128) or not (wq.is_contiguous()
+                                                                                     and ws.is_contiguous()):
+            raise ValueError("gemv_load_pattern: every weight set must be [N, K/8] codes and [N, K/128] scales")
+    if tuple(xq.shape) != (rows, K) or xq.element_size() != 1 or not xq.is_contiguous():
+        raise ValueError("gemv_load_pattern: xq must be int8 [rows, K]")
+    plan = rt4_amd.gemv_launch_plan(rows, N, K)
+    g = plan["groups_per_wave"]
+    if g not in (2, 4) or plan["row_blocks"] != 1 or K % (128 * g) or (g == 4 and plan["waves"] > 8):
+        return None
+    L = lib()
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for wq, ws in mats:
+            rc = L.rt4p_gemv_loads(P(wq), P(ws), P(xq), P(sink), rows, N, K, g, plan["waves"], plan["k_splits"],
+                                   cus, st)
+            if rc:
+                raise RuntimeError(f"rt4p_gemv_loads failed ({rc})")
+
+    fn()
+    torch.cuda.synchronize()
+    us = timed_graph(torch, fn) * 1e3 / len(mats)
+    return {"us": round(us, 3), "groups_per_wave": g, "waves": plan["waves"], "k_splits": plan["k_splits"]}
+
+
+def launch_cost(torch, timed_graph, n: int = 64) -> float:
+    """Microseconds per empty-kernel node in a graph of n back-to-back launches
+    (one workgroup of 64 threads each)."""
+    L = lib()
+
+    def fn():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _ in range(n):
+            if L.rt4p_empty(1, 64, st):
+                raise RuntimeError("rt4p_empty failed")
+
+    fn()
+    torch.cuda.synchronize()
+    return round(timed_graph(torch, fn) * 1e3 / n, 3)
+
+
+def mfma_f8f6f4_rates(torch, iters: int = 2048) -> dict:
+    """Measured dense rate (TOPS) of v_mfma_scale_f32_32x32x64_f8f6f4 with FP8, FP6 and
+    FP4 operands: 2 waves per SIMD, 4 independent accumulator chains per wave."""
+    L = lib()
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for fmt, name in ((0, "fp8"), (2, "fp6"), (4, "fp4")):
+        ms = _timed(torch, lambda: L.rt4p_mfma_f8f6f4(ctypes.c_void_p(sink.data_ptr()), fmt, iters, cus, st))
+        out[f"mfma_scale_32x32x64_{name}_TOPS"] = round(2.0 * 65536 * 4 * iters * 8 * cus / ms / 1e9, 1)
+    return out
+
+
+def gemm_unit_cycles(torch, units: int = 512) -> dict:
+    """The prefill GEMM's unit skeleton (rt4p_gemm_unit, registers only, 8 waves per
+    CU): nominal 2.4 GHz cycles per unit per SIMD (two waves' units), int8 form and
+    FP8-digit form, and the corresponding C2 gate/up time (21,760 units over the CUs)."""
+    L = lib()
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    units_c2 = (1024 // 128) * (17408 // 256) * (5120 // 128)
+    for variant, name in ((0, "int8"), (1, "fp8_digits")):
+        ms = _timed(torch, lambda: L.rt4p_gemm_unit(ctypes.c_void_p(sink.data_ptr()), variant, units, cus, st))
+        cyc = ms * 1e-3 * 2.4e9 / units
+        out[f"unit_{name}_cycles"] = round(cyc, 1)
+        out[f"unit_{name}_c2_gate_up_us"] = round(cyc * units_c2 / cus / 2.4e3, 1)
+    return out

@@ -40,7 +40,7 @@ import sys
 COPY_BYTES = 256 << 20            # bytes read and written by each probe copy launch
 COPY_KERNEL = "copy_k("          # the probe library's plain copy kernel
 KERNELS = {                       # report key -> substring of the rocprof kernel name
-    "gemv_gate_up": "gemv_w4a8_k<4",
+    "gemv_gate_up": "gemv_w4a8_tl_k<4",
     "gemm_gate_up": "gemm_w4a8_k<false>",
     "attention_c4": "fa_int4_k",
 }

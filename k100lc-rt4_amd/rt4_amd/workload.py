@@ -30,6 +30,9 @@ GEMM_SHAPES = {
     "c2_gate_up": (1024, 17408, 5120),
     "c2_down": (1024, 5120, 17408),
 }
+# The reference's own prefill GEMM benchmark shape (bench/int4_gemm2.cpp:4-9):
+# 2048 tokens against the 27B gate/up projection.
+GEMM_REF_SHAPE = (2048, 17408, 5120)
 
 
 def weights_np(rng: np.random.Generator, N: int, K: int):
@@ -85,6 +88,9 @@ def acts_torch(M: int, K: int, outliers: bool = False, device="cuda", generator=
 # 24 query heads, 4 KV heads (GQA 6:1), head dim 256, 1024 new query
 # rows over a 32768-token cache -> n_kv = 33792, query i at position 32768 + i.
 ATTN_C4 = {"H": 24, "KVH": 4, "D": 256, "n_q": 1024, "ctx": 32768}
+# The reference's own FlashAttention benchmark shape (docs/FLASH-ATTN.md:78-80): the
+# same heads, 1024 new query rows over a 131072-token cache.
+ATTN_REF = {"H": 24, "KVH": 4, "D": 256, "n_q": 1024, "ctx": 131072}
 
 
 def attn_np(rng: np.random.Generator, T: int, n_kv: int, H: int, KVH: int, D: int = 256):

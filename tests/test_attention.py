@@ -483,6 +483,23 @@ def test_attention_benchmark_shape_sampled(rt4, orc, torch_gpu):
 
 
 @pytest.mark.gpu
+def test_attention_reference_long_context_sampled(rt4, orc, torch_gpu):
+    """The reference's own benchmark shape (docs/FLASH-ATTN.md:78-80): 24 heads, GQA
+    6:1, 1024 queries over a 131072-token cache, sampled rows of the first and last
+    query head against the fp64 algorithm model."""
+    c = workload.ATTN_REF
+    n_q, ctx = c["n_q"], c["ctx"]
+    n_kv = ctx + n_q
+    print(f"case attention reference shape n_q={n_q} n_kv={n_kv}", flush=True)
+    rng = np.random.default_rng(15)
+    q, k, v = workload.attn_np(rng, n_q, n_kv, c["H"], c["KVH"])
+    rows = np.array([0, 511, 1023], np.int32)
+    out, _ = check_attention(rt4, orc, torch_gpu, q, k, v, c["H"] // c["KVH"], ctx, n_kv, n_kv,
+                             lambda h: rows, (0, 23))
+    assert np.isfinite(out).all()
+
+
+@pytest.mark.gpu
 def test_graph_keeps_workspace_when_scratch_grows(rt4, torch_gpu):
     """A HIP graph captured on the split-KV path holds the address of the library's
     partial-sum workspace.  A later, larger call grows that workspace; the graph's

@@ -93,6 +93,32 @@ def test_gemm_benchmark_shapes(rt4, orc, torch_gpu, name):
     assert worst < 1e-5  # bench/int4_gemm2.cpp:104-123
 
 
+def test_gemm_reference_benchmark_shape(rt4, orc, torch_gpu):
+    """The reference's own benchmark shape, M=2048 tokens x gate/up (bench/int4_gemm2.cpp:
+    4-9): sampled outputs against the fp64 oracle with the reference's criterion
+    (worst |err| / rms|c| < 1e-5), and the drop-in entry bit-identical to the int8 one."""
+    M, N, K = workload.GEMM_REF_SHAPE
+    print(f"case gemm reference shape M={M} N={N} K={K}", flush=True)
+    c, wq, ws, x = _case(torch_gpu, 3, M, N, K)
+    sb = rt4.make_group_major(ws, K)
+    xq, sc8 = rt4.quant_rows_i8(x)
+    y8 = host(rt4.gemm_w4a8_i8(wq, sb, xq, sc8))
+    qh, ql, sc, sc16 = rt4.quant_rows_a8(x)
+    y = host(rt4.gemm_w4a8(wq, sb, qh, ql, sc, sc16))
+    assert np.array_equal(y.view(np.uint32), y8.view(np.uint32)), "digit-plane and int8 entries differ"
+    rng = np.random.default_rng(9)
+    P = 4096
+    mi = rng.integers(0, M, P).astype(np.int32)
+    ni = rng.integers(0, N, P).astype(np.int32)
+    mi[:4], ni[:4] = [0, M - 1, 0, M - 1], [0, 0, N - 1, N - 1]
+    ref, _ = _oracle_points(orc, c, M, N, K, mi, ni)
+    got = y8[mi, ni]
+    err = rel_l2(got, ref)
+    worst = float(np.abs(got - ref).max()) / float(np.sqrt(np.mean(ref ** 2)))
+    print(f"  rel_l2 = {err:.3e}  worst/rms = {worst:.3e}")
+    assert err < TIGHT and worst < 1e-5
+
+
 def test_gemm_dropin_small_c2_uses_library_scratch(rt4, orc, torch_gpu):
     """4*N < K: the recombined codes do not fit in c2, library scratch is used."""
     M, N, K = 128, 64, 1024

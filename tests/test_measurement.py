@@ -58,7 +58,7 @@ def _write_csv(path, rows):
 
 def test_traffic_summary_scales_by_the_copy_calibration(tmp_path):
     from rt4_amd import profiling
-    gemv = "void rt4::(anonymous namespace)::gemv_w4a8_k<4, 2, 1, true, false, false>(...)"
+    gemv = "void rt4::(anonymous namespace)::gemv_w4a8_tl_k<4, false>(...)"
     copy = "void (anonymous namespace)::copy_k(uint4*, uint4 const*, unsigned long)"
     kib = profiling.COPY_BYTES // 1024
     # the copy reads COPY_BYTES but FETCH_SIZE reports half of it: scale 2; WRITE_SIZE exact
