@@ -386,9 +386,12 @@ def pattern_entry(pat: dict, nbytes: int, kernel_us: float) -> dict:
     time over it (the share of the GEMV that its load pattern accounts for)."""
     return {"us": pat["us"], "GBs": round(nbytes / pat["us"] / 1e3, 1),
             "frac": round(pat["us"] / kernel_us, 4),
-            "probe": f"rt4p_gemv_loads: the GEMV's grid and load form ({pat['groups_per_wave']} groups/wave, "
-                     f"{pat['waves']} waves, {pat['k_splits']} K pieces per leftover tile), weight/scale/activation "
-                     f"loads only, same weight sets back to back in a graph"}
+            "probe": ("rt4p_gemv_loads: the GEMV's grid and load form (" +
+                      (f"one-row dot-product form, 2 rows per wave, {pat['waves']} waves per workgroup"
+                       if pat["groups_per_wave"] == 0 else
+                       f"{pat['groups_per_wave']} groups/wave, {pat['waves']} waves, {pat['k_splits']} K pieces per "
+                       f"leftover tile") + "), weight/scale/activation loads only, same weight sets back to back in a "
+                      "graph")}
 
 
 def load_traffic(key: str):
@@ -586,7 +589,7 @@ def main() -> int:
                                   "probe": f"one-pass read of the same {gu_bytes} bytes (rt4p_read_burst, "
                                            f"{ceil_gu['blocks']}x{ceil_gu['threads']}, non-temporal), 16 buffers "
                                            f"back to back in a graph"}}
-    pat_gu = probe.gemv_load_pattern(torch, rt4_amd, gu_mats, xq_gu, M, timed_graph)
+    pat_gu = probe.gemv_load_pattern(torch, rt4_amd, gu_mats, xq_gu, sa_gu, M, timed_graph)
     if pat_gu:
         roofline["load_pattern"] = pattern_entry(pat_gu, gu_bytes, gu_us)
 
@@ -615,7 +618,7 @@ def main() -> int:
         kernels["gemv_down_m4"] = {"us": round(d_us, 3), "GBs": round(d_bytes / d_us / 1e3, 1),
                                    "measured_peak_GBs": ceil_d["GBs"],
                                    "frac_measured": round(d_bytes / d_us / 1e3 / ceil_d["GBs"], 4)}
-        pat_d = probe.gemv_load_pattern(torch, rt4_amd, d_mats, xq_d, M, timed_graph)
+        pat_d = probe.gemv_load_pattern(torch, rt4_amd, d_mats, xq_d, sa_d, M, timed_graph)
         if pat_d:
             kernels["gemv_down_m4"]["load_pattern"] = pattern_entry(pat_d, d_bytes, d_us)
 
@@ -647,7 +650,7 @@ def main() -> int:
         kernels["gemv_c0_m1"] = {"us": round(c0_us, 3), "GBs": round(c0_bytes / c0_us / 1e3, 1),
                                  "measured_peak_GBs": ceil_c0["GBs"], "measured_peak_us": ceil_c0["us"],
                                  "frac_measured": round(c0_bytes / c0_us / 1e3 / ceil_c0["GBs"], 4)}
-        pat_c0 = probe.gemv_load_pattern(torch, rt4_amd, c0_mats, xq1, 1, timed_graph)
+        pat_c0 = probe.gemv_load_pattern(torch, rt4_amd, c0_mats, xq1, sa1, 1, timed_graph)
         if pat_c0:
             kernels["gemv_c0_m1"]["load_pattern"] = pattern_entry(pat_c0, c0_bytes, c0_us)
         kernels["ceilings"] = {"mfma_i32_16x16x64_i8_TOPS": probe.mfma_i8_rate(torch),

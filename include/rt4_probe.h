@@ -39,10 +39,12 @@ int rt4p_valu_fma(void* sink, int iters, int blocks, void* stream);
 /* The decode GEMV's memory requests alone, for a launch plan (rt4_gemv_launch_plan)
  * of one 16-row block, `groups_per_wave` 2 (8 rows x 128 B per weight load, up to
  * 16 waves) or 4 (the row-transposed form, 4 rows x 256 B, up to 8 waves), `waves`
- * waves and `k_splits` pieces per leftover tile: wq/ws/xq as rt4_gemv_w4a8_q takes
- * them, `cus` the device's CU count.  rows 1..4, K a multiple of 128*groups_per_wave. */
-int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, void* sink, int rows, int N, int K,
-                    int groups_per_wave, int waves, int k_splits, int cus, void* stream);
+ * waves and `k_splits` pieces per leftover tile, or groups_per_wave 0: the one-row
+ * dot-product form (rows 1, K a multiple of 256 up to 8192, `waves` 1..4 per
+ * workgroup of two weight rows each).  wq/ws/xq/sa as rt4_gemv_w4a8_q takes them,
+ * `cus` the device's CU count.  rows 1..4, K a multiple of 128*groups_per_wave. */
+int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, const void* sa, void* sink, int rows, int N,
+                    int K, int groups_per_wave, int waves, int k_splits, int cus, void* stream);
 /* An empty kernel of `blocks` x `threads`. */
 int rt4p_empty(int blocks, int threads, void* stream);
 /* `iters` x 4 independent v_mfma_scale_f32_32x32x64_f8f6f4 per wave (65536 MACs

@@ -100,18 +100,22 @@ int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8
  * per workgroup.  When the tile count is not a multiple of the CU count, the
  * leftover tiles can be cut along K into pieces that run on otherwise idle
  * CUs: k_splits 1 keeps every tile whole, S >= 2 allows up to S pieces per
- * leftover tile.  0 selects the default for each parameter.  Configurations
- * differ only in the order of the fp32 sums over K groups; a configuration
- * gives the same y bit for bit on every call. */
+ * leftover tile.  0 selects the default for each parameter; all four 0 is the
+ * default launch, which for one activation row (K a multiple of 256, at most
+ * 8192) is a dot-product form outside this parameter space, and any non-zero
+ * parameter selects a tiled matrix-core form.  Configurations differ only in
+ * the order of the fp32 sums over K groups; a configuration gives the same y
+ * bit for bit on every call. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         int k_splits, int row_blocks, void* stream);
 
 /* The launch configuration rt4_gemv_w4a8_q picks for this shape on the
  * current device: groups per wave, waves per workgroup, the number of K
- * pieces per leftover tile (1: all tiles whole) and the 16-row blocks per tile.
- * No counterpart in the reference (its launch is fixed per M); for tuning and
- * reports. */
+ * pieces per leftover tile (1: all tiles whole) and the 16-row blocks per tile;
+ * groups_per_wave = row_blocks = 0 for the one-row dot-product form (waves: per
+ * workgroup, two weight rows each).  No counterpart in the reference (its
+ * launch is fixed per M); for tuning and reports. */
 int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* waves, int* k_splits,
                          int* row_blocks);
 

@@ -269,6 +269,7 @@ int gemv_cfg(const char* who, int K, int rows, int N, int groups_per_wave, int w
     }
     if (waves > 0) d.waves = waves;
     if (k_splits > 0) d.max_split = k_splits;
+    if (groups_per_wave > 0 || waves > 0 || k_splits > 0 || row_blocks > 0) d.dot = 0;   // an MFMA form
     if (!rt4::gemv_cfg_valid(d, K))
         return fail(RT4_E_ARG, "%s: bad config groups_per_wave=%d waves=%d k_splits=%d row_blocks=%d", who,
                     groups_per_wave, waves, k_splits, row_blocks);
@@ -398,10 +399,10 @@ int rt4_gemv_launch_plan(int rows, int N, int K, int* groups_per_wave, int* wave
     if (rc || (rc = device_cus(&cus))) return rc;
     const rt4::GemvCfg c = rt4::gemv_default_cfg(rows, N, K, cus);
     const rt4::GemvSplit sp = rt4::gemv_split(N, K, c, cus);
-    *groups_per_wave = c.gpw;
-    *waves = c.waves;
+    *groups_per_wave = c.dot ? 0 : c.gpw;   // 0: the dot-product form
+    *waves = c.dot ? rt4::kGemvDotWaves : c.waves;
     *k_splits = sp.nrem > 0 ? sp.S : 1;
-    *row_blocks = c.rb;
+    *row_blocks = c.dot ? 0 : c.rb;
     return RT4_OK;
 }
 

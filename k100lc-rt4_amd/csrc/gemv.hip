@@ -56,6 +56,15 @@
 //   values into the interleaved int8 operand in registers.  The dependent
 //   activation latency then hides under the weight stream instead of costing a
 //   launch of its own.  Codes and scales are bit-identical to quant_act_a8_k.
+//
+// Two further forms of the pre-quantized launch, chosen by the default plan:
+// * Row-transposed loads (gemv_w4a8_tl_k, 2-4 rows, K a multiple of 512): the
+//   4-group configuration with each load instruction covering 4 rows x 256 B,
+//   transposed to the operand layout through LDS; bit-identical to gemv_w4a8_k
+//   on that configuration.
+// * Dot products (gemv_w4a8_dot_k, one row, K a multiple of 256 up to 8192): each
+//   wave streams two whole weight rows 1 KB per instruction and folds per group
+//   with v_dot4_i32_i8 on the vector ALU.
 #include "rt4_dev.h"
 #include "rt4_internal.h"
 
@@ -643,6 +652,130 @@ __global__ __launch_bounds__(512) void gemv_w4a8_tl_k(const uint32_t* __restrict
     tile_finish<M, 1>(yacc, red, y, N, n0, W, w, lane, piece, b, rem, sp);
 }
 
+// ---- One activation row, row-contiguous dot products (DOT).  At M = 1 a 16-row
+// MFMA tile uses one of its 16 activation rows; here the vector ALU does the
+// arithmetic instead and the weight stream is laid out for the memory system
+// alone.  Each wave owns RPW consecutive weight rows, i.e. one contiguous span of
+// RPW*K/2 bytes, read 1 KB per load instruction (lane l of instruction i takes
+// bytes 16(64i + l) of the span), every instruction of a batch issued before the
+// first is used.  Rows are multiples of 64 B, so the four lanes of a quad always
+// hold the four 16-byte quarters of one 128-element group of one row:
+//   * lane: the 32 codes times the matching 32 activation codes (read from global
+//     memory, interleaved as quant_act_a8_k writes them: per 8 elements
+//     [c0 c2 c4 c6 c1 c3 c5 c7], the order of the even and odd nibbles), 8
+//     v_dot4_i32_i8 on the x16 nibble unpack -> 16 * its partial, exact;
+//   * quad: two DPP adds -> 16 * I[n][g] in all four lanes, exact;
+//   * quad leader: fp32(16 I) * (f16(ws)/16 * sa), the fold of gemv_w4a8_k, added
+//     to its row's fp32 partial; the wave then sums its 16 leaders per row.
+// No LDS, no cross-wave reduction and no K split; only the order of the fp32 sum
+// over groups differs from the MFMA forms.
+template <int RPW, int NI, bool GSUM>
+__global__ __launch_bounds__(256) void gemv_w4a8_dot_k(const uint32_t* __restrict__ wq,
+                                                       const uint16_t* __restrict__ ws,
+                                                       const int8_t* __restrict__ xq,
+                                                       const float* __restrict__ sa,
+                                                       float* __restrict__ y,
+                                                       int32_t* __restrict__ gsum, int N, int K) {
+    static_assert(RPW == 1 || RPW == 2, "one or two rows per wave");
+    const int lane = threadIdx.x & 63;
+    const int wv = uniform((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    const int NG = K >> 7, RS = K >> 1;
+    const int n0 = wv * RPW;
+    if (n0 >= N) return;                              // whole wave: no barrier follows
+    const int nrows = min(RPW, N - n0);
+    const int span = nrows * RS;                      // bytes, a multiple of 64; NI = ceil(RPW*RS/1024)
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(wq) + (size_t)n0 * RS;
+    const bool leader = (lane & 3) == 3;
+    // the wave's weight scales (nrows*NG fp16, contiguous) and the activation
+    // scales (NG floats), one dword per lane (RPW*NG <= 128), handed to the pieces
+    // with ds_bpermute; then every weight and activation load of the wave, in one
+    // straight-line block (a piece past the span -- the tail of the last
+    // instruction, or a short last wave -- reads the span's last piece again and is
+    // dropped)
+    const int nsw = (nrows * NG + 1) >> 1;
+    const uint32_t wsd = lane < nsw ? reinterpret_cast<const uint32_t*>(ws + (size_t)n0 * NG)[lane] : 0u;
+    const float sad = lane < NG ? sa[lane] : 0.f;
+    v4u w4[NI], x0[NI], x1[NI];
+    int rsv[NI], gv[NI];
+    bool okv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int ou = (i * 64 + lane) * 16;
+        okv[i] = ou < span;
+        const int o = okv[i] ? ou : span - 16;
+        rsv[i] = RPW == 2 && o >= RS ? 1 : 0;
+        const int br = o - rsv[i] * RS;               // byte in the row
+        gv[i] = br >> 6;
+        w4[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wb + o));
+        const v4u* xp = reinterpret_cast<const v4u*>(xq + (size_t)br * 2);
+        x0[i] = xp[0];
+        x1[i] = xp[1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        int I = 0;
+        I = __builtin_amdgcn_sdot4((int)even_x16(w4[i].x), (int)x0[i].x, I, false);
+        I = __builtin_amdgcn_sdot4((int)odd_x16(w4[i].x), (int)x0[i].y, I, false);
+        I = __builtin_amdgcn_sdot4((int)even_x16(w4[i].y), (int)x0[i].z, I, false);
+        I = __builtin_amdgcn_sdot4((int)odd_x16(w4[i].y), (int)x0[i].w, I, false);
+        I = __builtin_amdgcn_sdot4((int)even_x16(w4[i].z), (int)x1[i].x, I, false);
+        I = __builtin_amdgcn_sdot4((int)odd_x16(w4[i].z), (int)x1[i].y, I, false);
+        I = __builtin_amdgcn_sdot4((int)even_x16(w4[i].w), (int)x1[i].z, I, false);
+        I = __builtin_amdgcn_sdot4((int)odd_x16(w4[i].w), (int)x1[i].w, I, false);
+        I += (int)dpp<0xB1>((uint32_t)I);            // quad_perm [1,0,3,2]
+        I += (int)dpp<0x4E>((uint32_t)I);            // quad_perm [2,3,0,1]
+        const bool use = leader && okv[i];
+        if (GSUM && use) gsum[(size_t)(n0 + rsv[i]) * NG + gv[i]] = I >> 4;
+        const int h = rsv[i] * NG + gv[i];           // this piece's fp16 scale in the wave's list
+        const uint32_t pr = (uint32_t)__builtin_amdgcn_ds_bpermute((h >> 1) * 4, (int)wsd);
+        const float s_a = __int_as_float(__builtin_amdgcn_ds_bpermute(gv[i] * 4, __float_as_int(sad)));
+        // the fold of gemv_w4a8_k, fp32(16 I) * (f16(ws)/16 * sa), into this row's sum
+        // (a zero scale elsewhere: the term adds an exact zero)
+        const float sc = use ? f16_bits_to_f32((uint16_t)((h & 1) ? pr >> 16 : pr & 0xFFFFu)) * 0.0625f * s_a : 0.f;
+        acc0 = fmaf((float)I, RPW == 2 && rsv[i] ? 0.f : sc, acc0);
+        if (RPW == 2) acc1 = fmaf((float)I, rsv[i] ? sc : 0.f, acc1);
+        __builtin_amdgcn_sched_barrier(0);   // piece i's arithmetic waits for piece i's loads only
+    }
+    // sum of the 16 leaders (lanes 3, 7, ..., 63) per row: within each 16-lane row by
+    // two shifted adds (lane 15 of the row), then across rows by the two broadcasts
+    // (lane 63)
+    auto wave_sum = [&](float v) __attribute__((always_inline)) {
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xF, 0xF, true));   // row_shr:4
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xF, 0xF, true));   // row_shr:8
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));  // row_bcast:15
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));  // row_bcast:31
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    };
+    const float y0 = wave_sum(acc0);
+    const float y1 = RPW == 2 ? wave_sum(acc1) : 0.f;
+    if (lane == 0) {
+        y[n0] = y0;
+        if (RPW == 2 && nrows == 2) y[n0 + 1] = y1;
+    }
+}
+
+// Load instructions per wave of the dot-product form (1 KB each), at most this many
+// (128 registers of loads in flight per lane).
+constexpr int kDotMaxInst = 8;
+inline int dot_inst(int rpw, int K) { return (rpw * (K / 2) + 1023) / 1024; }
+
+template <int RPW, bool GSUM>
+hipError_t launch_dot(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
+                      const float* sa, int N, int K, int wpb, hipStream_t st) {
+    const int nw = (N + RPW - 1) / RPW, grid = (nw + wpb - 1) / wpb;
+    const dim3 g(grid), b(64 * wpb);
+    switch (dot_inst(RPW, K)) {
+#define RT4_DOT(NI) \
+    case NI: hipLaunchKernelGGL((gemv_w4a8_dot_k<RPW, NI, GSUM>), g, b, 0, st, wq, ws, xq, sa, y, gsum, N, K); break;
+        RT4_DOT(1) RT4_DOT(2) RT4_DOT(3) RT4_DOT(4) RT4_DOT(5) RT4_DOT(6) RT4_DOT(7) RT4_DOT(8)
+#undef RT4_DOT
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int M, int GPW, int RB, bool GSUM, bool QIN>
 hipError_t launch_one(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                       const float* sa, const float* xf, int N, int K, int waves, const GemvSplit& sp,
@@ -724,6 +857,16 @@ hipError_t launch_rows(float* y, int32_t* gsum, const uint32_t* wq, const uint16
 }  // namespace
 
 GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
+    // One activation row with K a multiple of 256 up to 8192: the dot-product form,
+    // two weight rows per wave.  Measured on MI355X (us, this form vs the MFMA rule
+    // below): K=5120 N=5120 4.9 vs 6.0, N=10240 6.9 vs 7.7, N=17408 9.9 vs 10.8;
+    // K=2048 N=8192 4.2 vs 4.8.  (One row per wave: 5.0, 10.6, 7.4, 4.1-4.4.)
+    GemvCfg c = gemv_mfma_cfg(rows, N, K, cus);
+    if (rows == 1 && K % 256 == 0 && K / kGroup <= 64 && dot_inst(2, K) <= kDotMaxInst) c.dot = 2;
+    return c;
+}
+
+GemvCfg gemv_mfma_cfg(int rows, int N, int K, int cus) {
     const int NG = K / kGroup;
     cus = cus > 0 ? cus : 256;
     GemvCfg c;
@@ -806,6 +949,11 @@ GemvSplit gemv_split(int N, int K, const GemvCfg& c, int cus) {
     // at least 32 groups (K = 17408 gains ~25%, K = 5120 loses ~5% when split).
     GemvSplit sp{};
     const int ntiles = (N + 16 * c.rb - 1) / (16 * c.rb);
+    if (c.dot) {                // the dot-product form is never split (nor is the fused
+        sp.full = ntiles;       // MFMA form that stands in for it)
+        sp.S = 1;
+        return sp;
+    }
     const int NC = (K / kGroup + c.gpw - 1) / c.gpw;
     cus = cus > 0 ? cus : 256;
     sp.full = ntiles / cus * cus;
@@ -832,6 +980,14 @@ size_t gemv_part_bytes(const GemvSplit& sp, int rows, int rb) {
 hipError_t launch_gemv_w4a8(float* y, int32_t* gsum, const uint32_t* wq, const uint16_t* ws,
                             const int8_t* xq, const float* sa, const float* xf, int rows, int N, int K,
                             const GemvCfg& cfg, const GemvSplit& sp, hipStream_t st) {
+    if (cfg.dot && !xf && rows == 1) {
+        if (dot_inst(cfg.dot, K) > kDotMaxInst || K % 256 || K / kGroup > 64) return hipErrorInvalidValue;
+        if (cfg.dot == 2)
+            return gsum ? launch_dot<2, true>(y, gsum, wq, ws, xq, sa, N, K, kGemvDotWaves, st)
+                        : launch_dot<2, false>(y, gsum, wq, ws, xq, sa, N, K, kGemvDotWaves, st);
+        return gsum ? launch_dot<1, true>(y, gsum, wq, ws, xq, sa, N, K, kGemvDotWaves, st)
+                    : launch_dot<1, false>(y, gsum, wq, ws, xq, sa, N, K, kGemvDotWaves, st);
+    }
     if (xf)  // the exact group sums are a test hook of the pre-quantized form only
         return gsum ? hipErrorInvalidValue
                     : launch_rows<false, true>(y, gsum, wq, ws, xq, sa, xf, rows, N, K, cfg, sp, st);

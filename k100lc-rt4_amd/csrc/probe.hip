@@ -18,8 +18,9 @@
 //                   grid (whole tiles plus K pieces of the leftover tiles), waves,
 //                   per-chunk weight-scale dwords (or the hoisted ones), line-wise
 //                   activation chunks and the non-temporal weight loads, in the
-//                   2-group form (8 rows x 128 B per load) or the row-transposed
-//                   4-group form (4 rows x 256 B); the loaded words are only
+//                   2-group form (8 rows x 128 B per load), the row-transposed
+//                   4-group form (4 rows x 256 B) or the one-row dot-product form
+//                   (two rows per wave, 1 KB per load); the loaded words are only
 //                   XOR-ed.  The gap between it and the GEMV is compute; the gap
 //                   between it and rt4p_read_burst is the access pattern
 //   rt4p_empty      an empty kernel: the per-launch cost of a graph node
@@ -285,6 +286,42 @@ __global__ __launch_bounds__(512) void gemv_loads_tl_k(const uint32_t* __restric
     if (acc == 0x9E3779B9u) sink[b] = acc;   // practically never: keeps the loads live
 }
 
+// The one-row dot-product GEMV's requests (gemv.hip gemv_w4a8_dot_k): two weight
+// rows per wave read as consecutive 1 KB load instructions, each lane's 32 matching
+// activation bytes, and the wave's scale dwords loaded once.
+template <int NI>
+__global__ __launch_bounds__(256) void gemv_loads_dot_k(const uint32_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                                                        const int8_t* __restrict__ xq, const float* __restrict__ sa,
+                                                        uint32_t* __restrict__ sink, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    const int NG = K >> 7, RS = K >> 1;
+    const int n0 = wv * 2;
+    if (n0 >= N) return;
+    const int nrows = min(2, N - n0);
+    const int span = nrows * RS;
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(wq) + (size_t)n0 * RS;
+    const int nsw = (nrows * NG + 1) >> 1;
+    uint32_t acc = lane < nsw ? reinterpret_cast<const uint32_t*>(ws + (size_t)n0 * NG)[lane] : 0u;
+    acc ^= lane < NG ? __float_as_uint(sa[lane]) : 0u;
+    v4u w4[NI], x0[NI], x1[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        int o = (i * 64 + lane) * 16;
+        o = o < span ? o : span - 16;
+        const int br = o >= RS ? o - RS : o;
+        w4[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(wb + o));
+        const v4u* xp = reinterpret_cast<const v4u*>(xq + (size_t)br * 2);
+        x0[i] = xp[0];
+        x1[i] = xp[1];
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+        acc ^= w4[i].x ^ w4[i].y ^ w4[i].z ^ w4[i].w ^ x0[i].x ^ x0[i].y ^ x0[i].z ^ x0[i].w ^ x1[i].x ^ x1[i].y ^
+               x1[i].z ^ x1[i].w;
+    if (acc == 0x9E3779B9u) sink[wv] = acc;   // practically never: keeps the loads live
+}
+
 template <int M>
 hipError_t launch_gemv_loads(const uint32_t* wq, const uint16_t* ws, const int8_t* xq, uint32_t* sink, int N, int K,
                              int waves, int full, int nrem, int S, size_t lds, bool hs, hipStream_t st) {
@@ -343,15 +380,21 @@ __global__ __launch_bounds__(512, 1) void gemm_unit_k(float* __restrict__ sink, 
     v16f S = zf, R[2] = {zf, zf};
     v16i I[2] = {zi, zi};
     for (int u = 0; u < units; u++) {
-        a4[0] ^= u;
-        a8[0] ^= u & 0x0f0f0f0f;
 #pragma unroll
         for (int ii = 0; ii < 4; ii++) {
             const int p = ii & 1, f = (ii + 3) & 3;
+            // operands distinct per row tile and unit: no MFMA of the unit may be
+            // merged with another or hoisted out of the loop
+            v4i a = a4;
+            a[1] ^= u * 4 + ii;
+            v8i a8u = a8;
+            a8u[1] ^= (u * 4 + ii) & 0x0f0f0f0f;
+            v4h sau = sa;
+            sau[0] ^= (short)(u * 4 + ii);
             if (VARIANT == 0) {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    I[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, k ? I[p] : zi, 0, 0, 0);
+                    I[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b4, k ? I[p] : zi, 0, 0, 0);
 #pragma unroll
                     for (int r = 4 * k; r < 4 * k + 4; r++) {
                         float v = fmaf((float)I[p ^ 1][r], S[r], facc[f][r]);
@@ -360,12 +403,12 @@ __global__ __launch_bounds__(512, 1) void gemm_unit_k(float* __restrict__ sink, 
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                S = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sa, sb, zf, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sau, sb, zf, 0, 0, 0);
             } else {
-                R[p] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sb, sa, zf, 0, 0, 0);   // the bias
+                R[p] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sb, sau, zf, 0, 0, 0);   // the bias
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    R[p] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, R[p], 0, 0, 0, 127, 0, 136);
+                    R[p] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8u, b8, R[p], 0, 0, 0, 127, 0, 136);
 #pragma unroll
                     for (int r = 4 * k; r < 4 * k + 4; r++) {
                         float v = fmaf(R[p ^ 1][r], S[r], facc[f][r]);
@@ -374,7 +417,7 @@ __global__ __launch_bounds__(512, 1) void gemm_unit_k(float* __restrict__ sink, 
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                S = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sa, sb, zf, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sau, sb, zf, 0, 0, 0);
             }
         }
     }
@@ -431,9 +474,30 @@ int rt4p_mfma_i8(void* sink, int big, int iters, int blocks, void* stream) {
     return last() == hipSuccess ? 0 : 3;
 }
 
-int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, void* sink, int rows, int N, int K,
-                    int groups_per_wave, int waves, int k_splits, int cus, void* stream) {
+int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, const void* sa, void* sink, int rows, int N,
+                    int K, int groups_per_wave, int waves, int k_splits, int cus, void* stream) {
     const int gpw = groups_per_wave;
+    if (gpw == 0) {   // the one-row dot-product form: two rows per wave, `waves` per workgroup
+        const int ni = (K + 1023) / 1024;
+        if (!wq || !ws || !xq || !sa || !sink || rows != 1 || N < 1 || K % 256 || K > 8192 || waves < 1 ||
+            waves > 4)
+            return 1;
+        const int nw = (N + 1) / 2, grid = (nw + waves - 1) / waves;
+        const uint32_t* w = static_cast<const uint32_t*>(wq);
+        const uint16_t* s = static_cast<const uint16_t*>(ws);
+        const int8_t* x = static_cast<const int8_t*>(xq);
+        const float* a = static_cast<const float*>(sa);
+        uint32_t* k = static_cast<uint32_t*>(sink);
+        hipStream_t st = (hipStream_t)stream;
+        switch (ni) {
+#define RT4P_DOT(NI) \
+    case NI: hipLaunchKernelGGL(gemv_loads_dot_k<NI>, dim3(grid), dim3(64 * waves), 0, st, w, s, x, a, k, N, K); break;
+            RT4P_DOT(1) RT4P_DOT(2) RT4P_DOT(3) RT4P_DOT(4) RT4P_DOT(5) RT4P_DOT(6) RT4P_DOT(7) RT4P_DOT(8)
+#undef RT4P_DOT
+            default: return 1;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : 3;
+    }
     if (!wq || !ws || !xq || !sink || rows < 1 || rows > 4 || N < 1 || (gpw != 2 && gpw != 4) || K < 128 * gpw ||
         K % (128 * gpw) || waves < 1 || waves > (gpw == 4 ? 8 : 16) || k_splits < 1 || cus < 1)
         return 1;

@@ -32,13 +32,17 @@ struct GemvCfg {
     int max_split;  // leftover tiles are cut along K into at most this many pieces (1: never,
                     // 0: as many as keep 32 groups per piece)
     int rb;     // 16-row blocks per tile (1 or 2): a wave applies its activations to rb blocks
+    int dot = 0;  // one activation row, pre-quantized: the row-contiguous dot-product form with
+                  // this many weight rows per wave (1 or 2); 0: the MFMA forms above
 };
 constexpr int kGemvMaxWaves = 16;
+constexpr int kGemvDotWaves = 2;       // waves per workgroup of the dot-product form
 constexpr int kGemvMaxSplit = 64;      // largest k_splits override
 constexpr int kGemvMaxRb = 2;
 constexpr int kGemvRb2MinRows = 3;     // default rb = 2 needs this many activation rows
 constexpr int kGemvRb2Work = 320;      // and this many (32-row tile x K group) units per CU
 GemvCfg gemv_default_cfg(int rows, int N, int K, int cus);
+GemvCfg gemv_mfma_cfg(int rows, int N, int K, int cus);   // the default among the MFMA forms
 bool gemv_cfg_valid(const GemvCfg& c, int K);
 // Grid of the GEMV: `full` whole tiles of 16*rb rows, then `nrem` tiles cut along
 // K into S pieces each, whose partials (part: nrem*S*rb*rows*16 floats) are summed

@@ -23,7 +23,7 @@ def lib() -> ctypes.CDLL:
         sigs = {"rt4p_hbm_read": [P, Z, P, I, P], "rt4p_read_burst": [P, Z, P, I, I, I, P],
                 "rt4p_copy": [P, P, Z, I, P],
                 "rt4p_mfma_i8": [P, I, I, I, P], "rt4p_valu_fma": [P, I, I, P],
-                "rt4p_gemv_loads": [P, P, P, P, I, I, I, I, I, I, I, P], "rt4p_empty": [I, I, P],
+                "rt4p_gemv_loads": [P, P, P, P, P, I, I, I, I, I, I, I, P], "rt4p_empty": [I, I, P],
                 "rt4p_mfma_f8f6f4": [P, I, I, I, P], "rt4p_gemm_unit": [P, I, I, I, P]}
         for name, args in sigs.items():
             getattr(L, name).argtypes = args
@@ -131,7 +131,7 @@ def mfma_i8_rate(torch, big: bool = False, iters: int = 2048) -> float:
     return round(2.0 * macs * 4 * iters * blocks * 4 / ms / 1e9, 1)
 
 
-def gemv_load_pattern(torch, rt4_amd, mats, xq, rows: int, timed_graph) -> dict | None:
+def gemv_load_pattern(torch, rt4_amd, mats, xq, sa, rows: int, timed_graph) -> dict | None:
     """The decode GEMV's memory requests alone (rt4p_gemv_loads) over the weight sets
     `mats` [(wq, ws)] with activations xq, back to back in a graph as the GEMV is
     timed: {"us": per launch, "groups_per_wave", "waves", "k_splits"}.  None when the
@@ -146,7 +146,10 @@ def gemv_load_pattern(torch, rt4_amd, mats, xq, rows: int, timed_graph) -> dict 
         raise ValueError("gemv_load_pattern: xq must be int8 [rows, K]")
     plan = rt4_amd.gemv_launch_plan(rows, N, K)
     g = plan["groups_per_wave"]
-    if g not in (2, 4) or plan["row_blocks"] != 1 or K % (128 * g) or (g == 4 and plan["waves"] > 8):
+    if g == 0:
+        if rows != 1 or K % 256 or K > 8192:
+            return None
+    elif g not in (2, 4) or plan["row_blocks"] != 1 or K % (128 * g) or (g == 4 and plan["waves"] > 8):
         return None
     L = lib()
     cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
@@ -156,8 +159,8 @@ def gemv_load_pattern(torch, rt4_amd, mats, xq, rows: int, timed_graph) -> dict 
     def fn():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         for wq, ws in mats:
-            rc = L.rt4p_gemv_loads(P(wq), P(ws), P(xq), P(sink), rows, N, K, g, plan["waves"], plan["k_splits"],
-                                   cus, st)
+            rc = L.rt4p_gemv_loads(P(wq), P(ws), P(xq), P(sa), P(sink), rows, N, K, g, plan["waves"],
+                                   plan["k_splits"], cus, st)
             if rc:
                 raise RuntimeError(f"rt4p_gemv_loads failed ({rc})")
 

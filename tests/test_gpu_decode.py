@@ -80,7 +80,8 @@ def _gemv_inputs(torch, seed, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (2, 40, 512), (3, 96, 1024), (4, 200, 2048),
                                    (4, 17, 128), (4, 1024, 5120), (3, 33, 384), (2, 48, 1920),
-                                   (4, 64, 40960), (1, 16, 128), (3, 65560, 384), (4, 70000, 256)])
+                                   (4, 64, 40960), (1, 16, 128), (3, 65560, 384), (4, 70000, 256),
+                                   (1, 1001, 8192), (1, 5120, 5120)])
 def test_gemv_groupsums_bit_exact(rt4, orc, torch_gpu, M, N, K):
     print(f"case gemv_groupsums M={M} N={N} K={K} plan={rt4.gemv_launch_plan(M, N, K)}", flush=True)
     c, wq, ws, x = _gemv_inputs(torch_gpu, 7, M, N, K)
@@ -100,9 +101,34 @@ def test_gemv_default_row_blocks(rt4, torch_gpu):
     shapes."""
     cus = torch_gpu.cuda.get_device_properties(0).multi_processor_count
     for M, N, K in [(4, 17408, 5120), (4, 5120, 17408), (4, 248320, 5120), (1, 248320, 5120),
-                    (3, 40960, 17408), (2, 248320, 5120)]:
-        want = 2 if M >= 3 and (N + 31) // 32 * (K // 128) >= 320 * cus else 1
+                    (3, 40960, 17408), (2, 248320, 5120), (1, 5120, 17408)]:
+        if M == 1 and K % 256 == 0 and K <= 8192:
+            want = 0                                  # the one-row dot-product form
+        else:
+            want = 2 if M >= 3 and (N + 31) // 32 * (K // 128) >= 320 * cus else 1
         assert rt4.gemv_launch_plan(M, N, K)["row_blocks"] == want, (M, N, K, cus)
+
+
+@pytest.mark.parametrize("N,K", [(1, 256), (3, 512), (100, 768), (5121, 5120), (257, 8192), (4096, 2048)])
+def test_gemv_one_row_dot_form(rt4, orc, torch_gpu, N, K):
+    """One activation row, K a multiple of 256 up to 8192: the default launch is the
+    row-contiguous dot-product form (two weight rows per wave, a short last wave at
+    odd N, partly used load instructions where a wave's rows are not a multiple of
+    1 KB).  Against the oracle and a tiled matrix-core launch of the same shape (the
+    fp32 group sums in another order), and repeatable bit for bit."""
+    print(f"case gemv_dot N={N} K={K}", flush=True)
+    plan = rt4.gemv_launch_plan(1, N, K)
+    assert plan["groups_per_wave"] == 0 and plan["row_blocks"] == 0, plan
+    c, wq, ws, x = _gemv_inputs(torch_gpu, 21, 1, N, K)
+    xq, sa = rt4.quant_act_a8(x)
+    y = rt4.gemv_w4a8_q(wq, ws, xq, sa)
+    y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa)
+    ym = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=2)
+    torch_gpu.cuda.synchronize()
+    ref = orc.gemv_w4a8(c["wq"], c["ws"], c["x"])
+    assert rel_l2(host(y), ref) < TIGHT
+    assert rel_l2(host(y), host(ym)) < TIGHT
+    assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
 
 
 @pytest.mark.parametrize("M,N,K,gpw,waves", [(4, 300, 3072, 4, 6), (1, 17, 128, 2, 1), (2, 40, 512, 4, 1),
@@ -218,7 +244,12 @@ def test_gemv_fused_quant_equals_two_launches(rt4, orc, torch_gpu, M, N, K, cfg)
     xq, sa = rt4.quant_act_a8(x)
     y2 = rt4.gemv_w4a8_q(wq, ws, xq, sa, groups_per_wave=g, waves=w, k_splits=s, row_blocks=rb)
     torch_gpu.cuda.synchronize()
-    assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
+    if cfg is None and rt4.gemv_launch_plan(M, N, K)["groups_per_wave"] == 0:
+        # the two-launch default is the one-row dot-product form, which the fused
+        # launch (a matrix-core form) does not share: same codes, other sum order
+        assert rel_l2(host(y), host(y2)) < TIGHT
+    else:
+        assert np.array_equal(host(y).view(np.uint32), host(y2).view(np.uint32))
     if N * K <= 5120 * 5120:
         ref = orc.gemv_w4a8(c["wq"], c["ws"], x_np)
         assert rel_l2(host(y), ref) < TIGHT
