@@ -82,11 +82,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the per-kernel table beyond the roofline")
     ap.add_argument("--pmc-probe", action="store_true",
-                    help="only launch the dominant kernels (gate/up GEMV, gate/up GEMM, C4 attention) and a "
-                         "calibration copy, eagerly (for rocprofv3 --pmc)")
+                    help="only launch the dominant kernels (gate/up and C0 GEMV, gate/up GEMM, C4 attention) and "
+                         "a calibration copy, eagerly (for rocprofv3 --pmc)")
     ap.add_argument("--only", choices=sorted(ONLY), default=None,
-                    help="only launch one kernel at one shape, eagerly, --steps times after 2 warm calls, and "
-                         "print its mean time (one rocprofv3 row per shape)")
+                    help="only launch one kernel at one shape: --steps launches in a graph, replayed for 300 ms, "
+                         "then timed once; prints their mean time (one rocprofv3 row per shape)")
     return ap.parse_args()
 
 
@@ -406,8 +406,8 @@ def load_traffic(key: str):
 
 def pmc_probe(torch, rt4_amd, workload, gen) -> int:
     """Eager launches for counter collection: the gate/up GEMV over 16 distinct weight
-    sets (twice), the gate/up prefill GEMM 3 times, the C4 attention prefill 3 times,
-    and 4 copies of COPY_BYTES."""
+    sets (twice), the C0 GEMV over 16 weight sets (twice), the gate/up prefill GEMM 3
+    times, the C4 attention prefill 3 times, and 4 copies of COPY_BYTES."""
     import ctypes
 
     from rt4_amd import probe, profiling
@@ -419,6 +419,12 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
     for _ in range(2):
         for wq, ws in mats:
             rt4_amd.gemv_w4a8_q(wq, ws, xq, sa, out=y)
+    # C0: one activation row over 5120 x 5120 slices of the same weight sets
+    xq1, sa1 = rt4_amd.quant_act_a8(workload.acts_torch(1, K, generator=gen))
+    y1 = torch.empty((1, 5120), device="cuda")
+    for _ in range(2):
+        for wq, ws in mats:
+            rt4_amd.gemv_w4a8_q(wq[:5120], ws[:5120], xq1, sa1, out=y1)
     del mats
     g = GemmCase(torch, rt4_amd, workload, gen, *workload.GEMM_SHAPES["c2_gate_up"])
     for _ in range(3):
@@ -443,35 +449,42 @@ def pmc_probe(torch, rt4_amd, workload, gen) -> int:
 
 
 def only_one(torch, rt4_amd, workload, gen, key: str, launches: int) -> int:
-    """Eager launches of one kernel at one shape (--only): 2 warm calls, then
-    `launches` calls timed together with events; prints one JSON line."""
+    """One kernel at one shape (--only), as bench.py times it: `launches` calls
+    captured in a HIP graph, replayed for 300 ms (clocks settle), then replayed once
+    more between two events; prints one JSON line.  In a kernel trace of this, the
+    last `launches` dispatches are the counted ones."""
     if key.startswith("gemm_"):
         shape = {"gemm_c2_gate_up": workload.GEMM_SHAPES["c2_gate_up"], "gemm_c2_down": workload.GEMM_SHAPES["c2_down"],
                  "gemm_ref_m2048": workload.GEMM_REF_SHAPE,
                  "gemm_dropin_c2_gate_up": workload.GEMM_SHAPES["c2_gate_up"]}[key]
         c = GemmCase(torch, rt4_amd, workload, gen, *shape)
-        fn = (lambda: c.dropin(rt4_amd)) if "dropin" in key else (lambda: c.int8(rt4_amd))
+        one = (lambda i: c.dropin(rt4_amd)) if "dropin" in key else (lambda i: c.int8(rt4_amd))
     elif key.startswith("attn_"):
         c = AttnCase(torch, rt4_amd, workload, gen, workload.ATTN_C4 if key == "attn_c4" else workload.ATTN_REF)
-        fn = lambda: c.fa(rt4_amd)  # noqa: E731
+        one = lambda i: c.fa(rt4_amd)  # noqa: E731
     else:
         M, N, K = (4, 17408, 5120) if key == "gemv_gate_up_m4" else (1, 5120, 5120)
         mats = [workload.weights_torch(N, K, generator=gen) for _ in range(16)]
         xq, sa = rt4_amd.quant_act_a8(workload.acts_torch(M, K, generator=gen))
         y = torch.empty((M, N), device="cuda")
-        it = iter(range(1 << 62))
-        fn = lambda: rt4_amd.gemv_w4a8_q(*mats[next(it) % 16], xq, sa, out=y)  # noqa: E731
-    for _ in range(2):
-        fn()
+        one = lambda i: rt4_amd.gemv_w4a8_q(*mats[i % 16], xq, sa, out=y)  # noqa: E731
+    one(0)                                   # eager first call: kernel attributes, workspaces
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(launches):
+            one(i)
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
-    for _ in range(launches):
-        fn()
+    g.replay()
     t1.record()
     torch.cuda.synchronize()
     print(json.dumps({"only": key, "what": ONLY[key], "launches": launches,
-                      "us_per_launch_eager": round(t0.elapsed_time(t1) * 1e3 / launches, 2)}), flush=True)
+                      "us_per_launch": round(t0.elapsed_time(t1) * 1e3 / launches, 2)}), flush=True)
     return 0
 
 

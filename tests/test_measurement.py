@@ -74,6 +74,27 @@ def test_traffic_summary_scales_by_the_copy_calibration(tmp_path):
     assert g["traffic_bytes"] == g["fetch_bytes"] + g["write_bytes"]
 
 
+def test_traffic_and_sq_markdown_carry_the_json_numbers(tmp_path):
+    """The markdown summaries are rendered from the same result dicts as the JSON."""
+    from rt4_amd import profiling
+    gemv = "void rt4::(anonymous namespace)::gemv_w4a8_tl_k<4, false>(...)"
+    copy = "void (anonymous namespace)::copy_k(uint4*, uint4 const*, unsigned long)"
+    kib = profiling.COPY_BYTES // 1024
+    _write_csv(tmp_path / "f.csv", [(copy, "FETCH_SIZE", kib), (gemv, "FETCH_SIZE", 45_000.0)])
+    _write_csv(tmp_path / "w.csv", [(copy, "WRITE_SIZE", kib), (gemv, "WRITE_SIZE", 300.0)])
+    res = profiling.summarize(str(tmp_path / "f.csv"), str(tmp_path / "w.csv"))
+    md = profiling.traffic_md(res, "f.csv", "w.csv")
+    g = res["gemv_gate_up"]
+    assert g["algorithmic_bytes"] == 46_256_768
+    assert f"{g['traffic_bytes']:,}" in md and f"{g['algorithmic_bytes']:,}" in md
+    assert profiling.attention_bytes(1024, 33792, 24, 4)["total"] == 69_500_928
+    rows = [(gemv, "SQ_WAVES", 100), (gemv, "SQ_INSTS_VALU", 100 * 50), (gemv, "SQ_INSTS_MFMA", 100 * 5)]
+    _write_csv(tmp_path / "a.csv", rows)
+    sq = profiling.summarize_sq([str(tmp_path / "a.csv")], 256)
+    md = profiling.sq_md(sq, "a.csv", "b.csv")
+    assert "| VALU per MFMA | 10.0 |" in md
+
+
 def test_sq_summary_fractions(tmp_path):
     from rt4_amd import profiling
     gemm = "void rt4::(anonymous namespace)::gemm_w4a8_k<false>(...)"
