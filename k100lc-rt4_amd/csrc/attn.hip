@@ -505,21 +505,23 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // -inf gives the same P there and also keeps a row that has seen nothing
         // yet -- possible at the start of a KV split -- at zero.)
         if (m < -1e29f) m = rref;
-        // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand.
-        // The clamp of the reference never binds here: m is the max of the row's S
-        // (fmaxf returns one of its operands), so S - m <= 0, 2^(S - m) is in [0, 1]
-        // (v_exp_f32 is within 1 ulp, and no value up to 8/7 could reach P = 8),
-        // and the truncation of 7*2^(S - m) + 0.5 lies in [0, 7]; a fully masked row
-        // has m = rref, S - m = -inf and P = 0.
+        // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand,
+        // with the 7 inside the exponent: 2^(S - (m - log2 7)).  That moves p by a
+        // few ulp, which can flip a code where 7 * 2^(S - m) + 0.5 lies within them
+        // of an integer, as the exp2 itself (v_exp_f32, within 1 ulp) already does
+        // against the reference's.  The clamp never binds: m is the max of the
+        // row's S (fmaxf returns one of its operands), so S - m <= 0 and p <= 7 (1 +
+        // a few ulp) < 7.5; a fully masked row has m = rref, S - m = -inf and P = 0.
+        const float m7 = m - 2.807354922057604f;   // m - log2(7)
         uint32_t pk[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             int pq[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                // v_exp_f32 directly: the arguments are <= 0 and any result below
-                // 2^-4 quantizes to P = 0, so denormal handling is irrelevant here
-                const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m) * 7.f;
+                // v_exp_f32 directly: the arguments are <= log2 7 and any result below
+                // 0.5 quantizes to P = 0, so denormal handling is irrelevant here
+                const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m7);
                 pq[r] = (int)(p + 0.5f);
             }
             pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[1] << 8 | (uint32_t)pq[2] << 16 | (uint32_t)pq[3] << 24;

@@ -223,26 +223,58 @@ __device__ __forceinline__ uint32_t swar_sub8(uint32_t x) {
     return ((x | 0x80808080u) - 0x08080808u) ^ (~x & 0x80808080u);
 }
 
+// One digit dword pair -> the 8 int8 codes of those 8 elements (interleaved order).
 template <bool HAS_H>
+__device__ __forceinline__ uint2 hl_pair(uint32_t h, uint32_t l) {
+    if (!HAS_H) h = 0u;
+    l ^= 0x88888888u;
+    const uint32_t xe = ((h << 4) & 0xF0F0F0F0u) | (l & 0x0F0F0F0Fu);
+    const uint32_t xo = (h & 0xF0F0F0F0u) | ((l >> 4) & 0x0F0F0F0Fu);
+    return make_uint2(swar_sub8(xe), swar_sub8(xo));
+}
+
+// VEC: four dwords of each plane per lane (16-byte loads, two 16-byte stores; all
+// three buffers 16-byte aligned), the last ndw % 4 dwords by the lane after the last
+// whole quad; otherwise one dword per lane.
+template <bool HAS_H, bool VEC>
 __global__ __launch_bounds__(256) void hl_to_i8_k(const uint32_t* __restrict__ qh,
                                                   const uint32_t* __restrict__ ql,
                                                   int8_t* __restrict__ xq, size_t ndw) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= ndw) return;
-    const uint32_t h = HAS_H ? qh[i] : 0u, l = ql[i] ^ 0x88888888u;
-    const uint32_t xe = ((h << 4) & 0xF0F0F0F0u) | (l & 0x0F0F0F0Fu);
-    const uint32_t xo = (h & 0xF0F0F0F0u) | ((l >> 4) & 0x0F0F0F0Fu);
-    reinterpret_cast<uint2*>(xq)[i] = make_uint2(swar_sub8(xe), swar_sub8(xo));
+    if constexpr (VEC) {
+        const size_t nq = ndw / 4;
+        if (i < nq) {
+            const uint4 l = reinterpret_cast<const uint4*>(ql)[i];
+            const uint4 h = HAS_H ? reinterpret_cast<const uint4*>(qh)[i] : make_uint4(0, 0, 0, 0);
+            const uint2 a = hl_pair<HAS_H>(h.x, l.x), b = hl_pair<HAS_H>(h.y, l.y);
+            const uint2 c = hl_pair<HAS_H>(h.z, l.z), d = hl_pair<HAS_H>(h.w, l.w);
+            uint4* o = reinterpret_cast<uint4*>(xq) + 2 * i;
+            o[0] = make_uint4(a.x, a.y, b.x, b.y);
+            o[1] = make_uint4(c.x, c.y, d.x, d.y);
+        } else if (i == nq) {
+            for (size_t j = 4 * nq; j < ndw; j++)
+                reinterpret_cast<uint2*>(xq)[j] = hl_pair<HAS_H>(HAS_H ? qh[j] : 0u, ql[j]);
+        }
+    } else {
+        if (i >= ndw) return;
+        reinterpret_cast<uint2*>(xq)[i] = hl_pair<HAS_H>(HAS_H ? qh[i] : 0u, ql[i]);
+    }
 }
 
 hipError_t launch_hl_to_i8(int8_t* xq, const uint32_t* qh, const uint32_t* ql, int rows, int K,
                            hipStream_t st) {
     const size_t ndw = (size_t)rows * (K / 8);
-    const unsigned blocks = (unsigned)((ndw + 255) / 256);
-    if (qh)
-        hipLaunchKernelGGL(hl_to_i8_k<true>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
-    else  // int4 codes alone (W4A4): sign-extended into the same interleaved int8 order
-        hipLaunchKernelGGL(hl_to_i8_k<false>, dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw);
+    const bool vec = ((uintptr_t)xq & 15) == 0 && ((uintptr_t)ql & 15) == 0 && ((uintptr_t)qh & 15) == 0;
+    const unsigned blocks = (unsigned)(((vec ? ndw / 4 + 1 : ndw) + 255) / 256);
+#define RT4_HL(H, V) hipLaunchKernelGGL((hl_to_i8_k<H, V>), dim3(blocks), dim3(256), 0, st, qh, ql, xq, ndw)
+    if (qh) {
+        if (vec) RT4_HL(true, true);
+        else RT4_HL(true, false);
+    } else {  // int4 codes alone (W4A4): sign-extended into the same interleaved int8 order
+        if (vec) RT4_HL(false, true);
+        else RT4_HL(false, false);
+    }
+#undef RT4_HL
     return hipGetLastError();
 }
 

@@ -72,6 +72,26 @@ def test_digits_to_i8_exhaustive(rt4, torch_gpu):
     assert np.array_equal(got.astype(int), q8)
 
 
+def test_digits_to_i8_tail_and_unaligned(rt4, torch_gpu):
+    """Four digit dwords per lane with the last ndw % 4 by one lane, and the
+    one-dword form for planes that are not 16-byte aligned: both equal 16h + l."""
+    rng = np.random.default_rng(8)
+    rows, K = 3, 40                       # 15 digit dwords: three whole quads and three more
+    h = rng.integers(-7, 7, size=(rows, K)).astype(np.int8)     # 16h + l stays in int8
+    l = rng.integers(-8, 8, size=(rows, K)).astype(np.int8)
+    want = 16 * h.astype(int) + l
+    qh, ql = layout.pack_rt4(h), layout.pack_rt4(l)
+    out = rt4.digits_to_i8(dev(torch_gpu, qh), dev(torch_gpu, ql))
+    bh = torch_gpu.zeros(qh.size + 1, dtype=torch_gpu.int32, device="cuda")
+    bl = torch_gpu.zeros(ql.size + 1, dtype=torch_gpu.int32, device="cuda")
+    bh[1:].copy_(dev(torch_gpu, qh).view(-1))
+    bl[1:].copy_(dev(torch_gpu, ql).view(-1))
+    out_u = rt4.digits_to_i8(bh[1:].view(rows, K // 8), bl[1:].view(rows, K // 8))   # 4-byte offset
+    torch_gpu.cuda.synchronize()
+    assert np.array_equal(layout.deinterleave(host(out)).astype(int), want)
+    assert np.array_equal(host(out_u), host(out))
+
+
 @pytest.mark.parametrize("rows,K,G", [(128, 5120, 128), (64, 512, 32)])
 def test_quant_rows_a4_bit_exact(rt4, orc, torch_gpu, rows, K, G):
     x = workload.acts_np(np.random.default_rng(7), rows, K)
