@@ -29,9 +29,9 @@
  *                          row-major (the reference passes these as `const float*`).
  *   wsc_gm float [K/128][N] fp32 group-major weight scales (src/model.cpp:190-202):
  *                          the fp16 scales of ws widened to fp32, as
- *                          rt4_make_group_major writes them.  The prefill GEMMs
- *                          use them as such (11 significant bits); other fp32
- *                          values would count to 16 significant bits.
+ *                          rt4_make_group_major writes them, or any other finite
+ *                          fp32 values: the prefill GEMMs keep all 24 significant
+ *                          bits in their scale products.
  *   xq   int8  [rows][K]   activation codes in "interleaved" order: for each
  *                          8-element block b, bytes [a(8b+0) a(8b+2) a(8b+4) a(8b+6)
  *                          a(8b+1) a(8b+3) a(8b+5) a(8b+7)].  Internal to this
@@ -102,10 +102,10 @@ int rt4_gemv_w4a8_q(float* y, const uint32_t* wq, const uint16_t* ws, const int8
  * CUs: k_splits 1 keeps every tile whole, S >= 2 allows up to S pieces per
  * leftover tile.  0 selects the default for each parameter; all four 0 is the
  * default launch, which for one activation row (K a multiple of 256, at most
- * 8192) is a dot-product form outside this parameter space, and any non-zero
- * parameter selects a tiled matrix-core form.  Configurations differ only in
- * the order of the fp32 sums over K groups; a configuration gives the same y
- * bit for bit on every call. */
+ * 8192, N at most 256 rows per CU) is a dot-product form outside this parameter
+ * space, and any non-zero parameter selects a tiled matrix-core form.
+ * Configurations differ only in the order of the fp32 sums over K groups; a
+ * configuration gives the same y bit for bit on every call. */
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         int k_splits, int row_blocks, void* stream);

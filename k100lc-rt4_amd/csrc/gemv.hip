@@ -857,12 +857,18 @@ hipError_t launch_rows(float* y, int32_t* gsum, const uint32_t* wq, const uint16
 }  // namespace
 
 GemvCfg gemv_default_cfg(int rows, int N, int K, int cus) {
-    // One activation row with K a multiple of 256 up to 8192: the dot-product form,
-    // two weight rows per wave.  Measured on MI355X (us, this form vs the MFMA rule
-    // below): K=5120 N=5120 4.9 vs 6.0, N=10240 6.9 vs 7.7, N=17408 9.9 vs 10.8;
-    // K=2048 N=8192 4.2 vs 4.8.  (One row per wave: 5.0, 10.6, 7.4, 4.1-4.4.)
+    // One activation row with K a multiple of 256 up to 8192 and at most 16 tiles of
+    // 16 rows per CU: the dot-product form, two weight rows per wave.  Measured on
+    // MI355X (us, this form vs the MFMA rule below): K=5120 N=5120 4.9 vs 6.0,
+    // N=10240 6.9 vs 7.7, N=17408 9.9 vs 10.8; K=2048 N=8192 4.2 vs 4.8; K=4096
+    // N=14336 8.0 vs 8.2; K=8192 N=8192 8.3 vs 9.3, N=28672 20.7 vs 24.3.  (One row
+    // per wave: 5.0, 10.6, 7.4, 4.1-4.4.)  At the LM head (N=248320, 61 tiles per
+    // CU) its 124,160 small waves lose: 112.4 vs 96.9 us.
     GemvCfg c = gemv_mfma_cfg(rows, N, K, cus);
-    if (rows == 1 && K % 256 == 0 && K / kGroup <= 64 && dot_inst(2, K) <= kDotMaxInst) c.dot = 2;
+    const int ncu = cus > 0 ? cus : 256;
+    if (rows == 1 && K % 256 == 0 && K / kGroup <= 64 && dot_inst(2, K) <= kDotMaxInst &&
+        (N + 15) / 16 <= 16 * ncu)
+        c.dot = 2;
     return c;
 }
 
