@@ -18,30 +18,49 @@
 // O = O·alpha + (Σ_k P·Vcode)·(beta/7)·vsc; out = O / L.
 //
 // MI355X design.  A workgroup is 64 query rows of one head, 4 waves of 16 rows.
-// Both contractions run on v_mfma_i32_16x16x64_i8 in transposed form so that a
-// lane always owns one query row:
-//   S^T[key][q] = K·Q^T   A = K codes (x16 unpack), B = the wave's Q codes
-//                         (resident, sign-extended int8); a lane holds query
-//                         q = lane%16 and, in register r of subtile t, key
-//                         16t + 8(G/2) + 2r + G%2 (G = lane/16): the K rows are
-//                         fed in that order, so lane group G holds the even
-//                         (G even) or odd keys of one 8-key group.
-//   O^T[d][q]  = V^T·P^T  B = P straight from those registers (4 dwords: the
-//                         lane's 16 keys), A = V codes laid out in LDS with the
-//                         same key order, so P never leaves the registers; with
-//                         that order a V operand dword is exactly the x16 even-
+// Both contractions run on v_mfma_f32_16x16x128_f8f6f4 with FP8 E4M3 operands
+// that hold the integer codes exactly, so the products come out as fp32 with no
+// int-to-float conversion:
+//   - K and V codes c enter as the byte c + 8 (the nibble xor 8), which is the
+//     E4M3 encoding of (c + 8)·2^-9: the subnormals 0..7 and the first normal
+//     binade 8..15 are spaced 2^-9 apart.  The offset's contribution, 8 times the
+//     other operand's sum, is taken off through the accumulator input C.
+//   - Q codes enter as their exact E4M3 values (converted once), P codes 0..7 as
+//     the subnormals p·2^-9, which v_cvt_scalef32_pk_fp8_f32 (scale 512) produces
+//     from p rounded to the nearest code.
+// Every partial sum is an integer times a power of two below 2^24, so each
+// MFMA result is exact.  The contractions are in transposed form so that a lane
+// always owns one query row:
+//   S^T[key][q] = K·Q^T   one MFMA per subtile of 16 keys and 128-dim group
+//                         (K = 128 is the quantization group), A = K operand
+//                         bytes, B = the wave's resident Q bytes, C = -8·Σq·2^-9;
+//                         result I·2^-9.  A lane holds query q = lane%16 and, in
+//                         register r of subtile t, key 16t + 8(G/2) + 2r + G%2
+//                         (G = lane/16): the K rows are fed in that order, so
+//                         lane group G holds the even (G even) or odd keys of
+//                         one 8-key group.
+//   O^T[d][q]  = V^T·P^T  the 64 keys of a tile fill half of K = 128: B = P
+//                         straight from those registers (the lane's 16 keys) in
+//                         one half and zeros in the other, A = the V operands of
+//                         two dim tiles laid out in LDS with the same key order
+//                         (one per half), so one A register block serves two
+//                         MFMAs; C = -8·ΣP·2^-18 from a fifth MFMA against
+//                         -2^-6 bytes, which also gives the row sum of P.  With
+//                         that key order a V operand dword is exactly the even-
 //                         or odd-key bytes of one V cache dword.
-// Row max and row sum over a query's 64 keys are 15 in-lane ops plus two
-// cross-lane steps (xor 16, xor 32).  The workgroup unpacks each K/V tile once
-// into LDS in MFMA operand order (x16 bytes per (subtile, k-step, lane)), so the
-// waves only issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
+// Row max over a query's 64 keys is 15 in-lane ops plus two cross-lane steps
+// (xor 16, xor 32).  The workgroup unpacks each K/V tile once into LDS in MFMA
+// operand order (16 bytes per (subtile, group, half, lane)), so the waves only
+// issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.  The tile loop is a two-tile
 // pipeline (S and P of the next tile beside the PV product of the current one;
 // see the loop), the scale products of both contractions run on
 // v_mfma_f32_16x16x1f32 (four 16x16 tiles per instruction: 2 per tile for S, 4
 // for O; four v_mfma_f32_4x4x1f32 cost about twice the matrix-core time of one),
-// and K/V are read with range-checked buffer loads.
+// and K/V are read with range-checked buffer loads.  The power-of-two factors of
+// the operand encodings (2^-9 for S, 2^-18 for O) are folded into the Q scale and
+// the P scale, so every rounded operation is the one the integer form had.
 #include <type_traits>
 
 #include "rt4_dev.h"
@@ -62,6 +81,27 @@ constexpr int VU_BYTES = 16 * 64 * 16;      // unpacked V operands of one tile
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef short v2s __attribute__((ext_vector_type(2)));
+
+// D = A·B + C on 16x16x128 FP8 E4M3 operands (format 0 for both, no block scale).
+__device__ __forceinline__ v4f mfma_e4m3(v8i a, v8i b, v4f c) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+__device__ __forceinline__ v8i cat8(v4i lo, v4i hi) {
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// Offset-code bytes of one code dword w8 = w ^ 0x88888888 (every nibble c -> c + 8):
+// nibbles 0, 2, 4, 6 (even) or 1, 3, 5, 7 (odd) as the bytes c + 8 = E4M3 of (c + 8)·2^-9.
+__device__ __forceinline__ uint32_t even_e4m3(uint32_t w8) { return w8 & 0x0F0F0F0Fu; }
+__device__ __forceinline__ uint32_t odd_e4m3(uint32_t w8) { return (w8 >> 4) & 0x0F0F0F0Fu; }
+// E4M3 encoding of an integer -8..8: magnitudes 0..7 are the bytes 00 38 40 44 48
+// 4A 4C 4E (exponent bias 7, 3 mantissa bits), 8 is 0x50; sign in bit 7.
+__device__ __forceinline__ uint32_t e4m3_of_int(int c) {
+    const uint32_t m = (uint32_t)(c < 0 ? -c : c);
+    const uint32_t b = m < 8 ? (uint32_t)(0x4E4C4A4844403800ull >> (8 * m)) & 0xFFu : 0x50u;
+    return b | (c < 0 ? 0x80u : 0u);
+}
 
 // Key order within a 16-key subtile: output register r of lane group G holds key
 // key_of_slot(G, r); the K row fed to the MFMA at slot 4G + r is that key.
@@ -81,16 +121,6 @@ __device__ __forceinline__ v16f outer16(float x_of_lane, float y) {
 }
 
 __device__ __forceinline__ int sext4(uint32_t w, int e) { return ((int)(w << (28 - 4 * e))) >> 28; }
-
-// Sign-extended int8 codes of one dword in the interleaved order [c0 c2 c4 c6 | c1 c3 c5 c7].
-__device__ __forceinline__ uint2 codes_i8(uint32_t w) {
-    uint2 r;
-    r.x = (uint32_t)(sext4(w, 0) & 0xFF) | (uint32_t)(sext4(w, 2) & 0xFF) << 8 |
-          (uint32_t)(sext4(w, 4) & 0xFF) << 16 | (uint32_t)(sext4(w, 6) & 0xFF) << 24;
-    r.y = (uint32_t)(sext4(w, 1) & 0xFF) | (uint32_t)(sext4(w, 3) & 0xFF) << 8 |
-          (uint32_t)(sext4(w, 5) & 0xFF) << 16 | (uint32_t)(sext4(w, 7) & 0xFF) << 24;
-    return r;
-}
 
 // int4 code of x / s (s = amax/7 or 1), same IEEE ops as the reference quantizers.
 __device__ __forceinline__ uint32_t code4(float x, float s) {
@@ -339,16 +369,36 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     const int split = blockIdx.z;
     const int t0 = (int)((long long)nt * split / nsplit), t1 = (int)((long long)nt * (split + 1) / nsplit);
 
-    // resident Q operand: k-step s covers dims 64s + 16G .. +15 (dwords 8s+2G, 8s+2G+1)
-    v4i qop[4];
+    // Resident Q operand of group g: dims 128g + 32G .. +31, the 4 code dwords w_m
+    // (dims 8m..8m+7 of that range) as E4M3 bytes in the order even(w0) odd(w0)
+    // even(w1) ... odd(w3), the order the K operand bytes are staged in.  cS[g] =
+    // -8·Σq·2^-9 over the group's 128 dims takes the K offset back off.
+    v8i qop[2];
+    float cS[2];
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint2 wd = *reinterpret_cast<const uint2*>(qq + (size_t)qrow * KDW + 8 * s + 2 * G);
-        const uint2 a = codes_i8(wd.x), b = codes_i8(wd.y);
-        qop[s] = v4i{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
+    for (int g = 0; g < 2; g++) {
+        const uint4 wd = *reinterpret_cast<const uint4*>(qq + (size_t)qrow * KDW + 16 * g + 4 * G);
+        const uint32_t w[4] = {wd.x, wd.y, wd.z, wd.w};
+        int qs = 0;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            uint32_t ev = 0, od = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int ce = sext4(w[m], 2 * j), co = sext4(w[m], 2 * j + 1);
+                qs += ce + co;
+                ev |= e4m3_of_int(ce) << (8 * j);
+                od |= e4m3_of_int(co) << (8 * j);
+            }
+            qop[g][2 * m] = (int)ev;
+            qop[g][2 * m + 1] = (int)od;
+        }
+        qs += __shfl_xor(qs, 16);
+        qs += __shfl_xor(qs, 32);
+        cS[g] = (float)(-8 * qs) * (1.f / 512.f);
     }
-    // S in log2 units: fold log2(e) and the 1/16 of the x16 K operand into the Q scales
-    const float A0 = qsc[qrow] * (L2E * 0.0625f), A1 = qsc[n_q + qrow] * (L2E * 0.0625f);
+    // S in log2 units: fold log2(e) and the 2^9 of the offset K operand into the Q scales
+    const float A0 = qsc[qrow] * (L2E * 512.f), A1 = qsc[n_q + qrow] * (L2E * 512.f);
 
     float O[16][4];
 #pragma unroll
@@ -416,30 +466,37 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         S.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_vs, tid * 4, t * HD * 4, 0));
     };
     auto store_k = [&](const StageK& S, int b, int t) {
-        // x16 bytes of dwords (8p + 2g, 8p + 2g + 1) for lane g*16 + slot of kk%16 in
-        // subtile kk/16; keys >= n_kv read as zero codes (flash_attn_core.h:143-147)
+        // Key kk, dims 64p .. 64p + 63 (code dwords j = 0..7): group p/2, lane group
+        // G' = 2(p%2) + j/4 of the operand, half (j/2)%2 of its 32 bytes.  Piece
+        // (subtile, group, half) is 64 lanes x 16 bytes; the key's lane in it is
+        // 16G' + slot of kk%16.  Keys >= n_kv read as zero codes
+        // (flash_attn_core.h:143-147), i.e. bytes 8.
         unsigned char* kub = ku + b * KU_BYTES;
         const int kk = tid & 63, p = tid >> 6;
-        const uint32_t d[8] = {S.k0.x, S.k0.y, S.k0.z, S.k0.w, S.k1.x, S.k1.y, S.k1.z, S.k1.w};
+        const uint32_t d[8] = {S.k0.x ^ 0x88888888u, S.k0.y ^ 0x88888888u, S.k0.z ^ 0x88888888u,
+                               S.k0.w ^ 0x88888888u, S.k1.x ^ 0x88888888u, S.k1.y ^ 0x88888888u,
+                               S.k1.z ^ 0x88888888u, S.k1.w ^ 0x88888888u};
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const uint4 v = make_uint4(even_x16(d[2 * g]), odd_x16(d[2 * g]), even_x16(d[2 * g + 1]),
-                                       odd_x16(d[2 * g + 1]));
-            *reinterpret_cast<uint4*>(kub + (((kk >> 4) * 4 + p) * 64 + g * 16 + slot_of_key(kk & 15)) * 16) = v;
+            const uint4 v = make_uint4(even_e4m3(d[2 * g]), odd_e4m3(d[2 * g]), even_e4m3(d[2 * g + 1]),
+                                       odd_e4m3(d[2 * g + 1]));
+            const int piece = ((kk >> 4) * 2 + (p >> 1)) * 2 + (g & 1);
+            *reinterpret_cast<uint4*>(kub + (piece * 64 + 16 * (2 * (p & 1) + (g >> 1)) + slot_of_key(kk & 15)) * 16) = v;
         }
         if (tid < 2 * BNK) ks_l[b][tid] = t * BNK + (tid & 63) < kv_cap ? S.ks : 1.f;
     };
     auto store_v = [&](const StageV& S, int b, int t) {
-        // lane G*16 + d%16 of dim tile d/16 gets, in dword t = 0..3, the x16 bytes of
-        // the even (G even) or odd keys of 8-key group 2t + G/2 -- keys
+        // lane G*16 + d%16 of dim tile d/16 gets, in dword t = 0..3, the offset-code
+        // bytes of the even (G even) or odd keys of 8-key group 2t + G/2 -- keys
         // 16t + key_of_slot(G, r), r = 0..3, as P holds them; a group of 8 keys is
-        // read only if it is whole (flash_attn_core.h:150-152)
+        // read only if it is whole (flash_attn_core.h:150-152), else zero codes
         unsigned char* vub = vu + b * VU_BYTES;
         uint32_t e[8], o[8];
 #pragma unroll
         for (int g = 0; g < 8; g++) {
-            e[g] = even_x16(S.v[g]);
-            o[g] = odd_x16(S.v[g]);
+            const uint32_t w8 = S.v[g] ^ 0x88888888u;
+            e[g] = even_e4m3(w8);
+            o[g] = odd_e4m3(w8);
         }
 #pragma unroll
         for (int G = 0; G < 4; G++) {
@@ -451,13 +508,14 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     };
 
     const v4i zero = {0, 0, 0, 0};
+    const v4f cS0 = {cS[0], cS[0], cS[0], cS[0]}, cS1 = {cS[1], cS[1], cS[1], cS[1]};
     // front of tile t (K in buffer b): S^T = K Q^T for the 4 subtiles of 16 keys,
     // the causal mask (MASK: the tile may reach past a row of this workgroup), the
-    // tile max m of each row, the P codes as the PV operand and their row sum.
+    // tile max m of each row, the P codes as the PV operand and -8·ΣP·2^-18.
     struct Front {
         v4i pop;
         float m;
-        int isum;
+        v4f corr;       // the same value in all four registers (every output row)
     };
     auto front = [&](int t, int b, auto mask_tag) -> Front {
         constexpr bool MASK = decltype(mask_tag)::value;
@@ -470,13 +528,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const v16f c1 = outer16(ksb[BNK + kslot], A1);
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
+            // pieces (kt, group, half) at ((kt * 2 + group) * 2 + half) * 64
             const v4i* kp = reinterpret_cast<const v4i*>(kub) + (kt * 4) * 64 + lane;
-            v4i a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[0], qop[0], zero, 0, 0, 0);
-            a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[64], qop[1], a0, 0, 0, 0);
-            v4i a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[128], qop[2], zero, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kp[192], qop[3], a1, 0, 0, 0);
+            const v4f a0 = mfma_e4m3(cat8(kp[0], kp[64]), qop[0], cS0);
+            const v4f a1 = mfma_e4m3(cat8(kp[128], kp[192]), qop[1], cS1);
 #pragma unroll
-            for (int r = 0; r < 4; r++) sv[kt][r] = fmaf((float)a1[r], c1[4 * kt + r], (float)a0[r] * c0[4 * kt + r]);
+            for (int r = 0; r < 4; r++) sv[kt][r] = fmaf(a1[r], c1[4 * kt + r], a0[r] * c0[4 * kt + r]);
         }
         if constexpr (MASK) {
             if (kb + BNK - 1 > off + q0 + 16 * w) {     // this wave has masked entries in the tile
@@ -506,38 +563,44 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // yet -- possible at the start of a KV split -- at zero.)
         if (m < -1e29f) m = rref;
         // ---- P = clamp(int(7 * 2^(S - m) + 0.5), 0, 7), packed as the PV operand,
-        // with the 7 inside the exponent: 2^(S - (m - log2 7)).  That moves p by a
-        // few ulp, which can flip a code where 7 * 2^(S - m) + 0.5 lies within them
+        // with the 7 inside the exponent: p = 2^(S - (m - log2 7)).  That moves p by
+        // a few ulp, which can flip a code where 7 * 2^(S - m) + 0.5 lies within them
         // of an integer, as the exp2 itself (v_exp_f32, within 1 ulp) already does
-        // against the reference's.  The clamp never binds: m is the max of the
-        // row's S (fmaxf returns one of its operands), so S - m <= 0 and p <= 7 (1 +
-        // a few ulp) < 7.5; a fully masked row has m = rref, S - m = -inf and P = 0.
+        // against the reference's.  v_cvt_scalef32_pk_fp8_f32 with scale 512 gives
+        // the E4M3 byte of p/512 rounded to the nearest subnormal, i.e. p rounded to
+        // the nearest integer code, as the byte of that code (ties go to even where
+        // the reference rounds up: p exactly k + 1/2, inside the few-ulp band above).
+        // The clamp never binds: m is the max of the row's S (fmaxf returns one of
+        // its operands), so S - m <= 0 and p <= 7 (1 + a few ulp) < 7.5; a fully
+        // masked row has m = rref, S - m = -inf and P = 0.
         const float m7 = m - 2.807354922057604f;   // m - log2(7)
         uint32_t pk[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
-            int pq[4];
+            // v_exp_f32 directly: the arguments are <= log2 7 and any result below
+            // 0.5 converts to code 0, so denormal handling is irrelevant here
+            float p[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                // v_exp_f32 directly: the arguments are <= log2 7 and any result below
-                // 0.5 quantizes to P = 0, so denormal handling is irrelevant here
-                const float p = __builtin_amdgcn_exp2f(sv[kt][r] - m7);
-                pq[r] = (int)(p + 0.5f);
-            }
-            pk[kt] = (uint32_t)pq[0] | (uint32_t)pq[1] << 8 | (uint32_t)pq[2] << 16 | (uint32_t)pq[3] << 24;
+            for (int r = 0; r < 4; r++) p[r] = __builtin_amdgcn_exp2f(sv[kt][r] - m7);
+            v2s w;
+            asm volatile("" : "=v"(w));          // both halves are written below
+            w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, p[0], p[1], 512.f, false);
+            w = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(w, p[2], p[3], 512.f, true);
+            pk[kt] = __builtin_bit_cast(uint32_t, w);
         }
         Front f;
         f.pop = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
         f.m = m;
-        // Σ_k P of the row over the tile's 64 keys on the matrix pipe: an A operand
-        // of ones gives it in every output row (exact integers)
-        const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-        f.isum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ones, f.pop, zero, 0, 0, 0)[0];
+        // -8·Σ_k P·2^-18 of the row over the tile's 64 keys on the matrix pipe: A
+        // bytes -2^-6 (E4M3 0x88) against the P half give it in every output row
+        const v8i neg8 = {(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888,
+                          (int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};
+        f.corr = mfma_e4m3(neg8, cat8(f.pop, zero), v4f{0.f, 0.f, 0.f, 0.f});
         return f;
     };
-    // Online update with a tile's (m, row sum): the running reference, L, and O
-    // rescaled by alpha.  Returns the P scale beta/7 times the 1/16 of the x16 V
-    // operand.
+    // Online update with a tile's (m, -8·ΣP·2^-18): the running reference, L, and O
+    // rescaled by alpha.  Returns the P scale beta/7 times the 2^18 of the PV
+    // operand bytes.
     auto update = [&](const Front& f) -> float {
         const float r_new = fmaxf(rref, f.m);
         // v_exp_f32 directly: both arguments are <= 0, and a factor below 2^-126
@@ -545,7 +608,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const float alpha = __builtin_amdgcn_exp2f(rref - r_new);
         const float beta = __builtin_amdgcn_exp2f(f.m - r_new);
         const float pb = beta * (1.f / 7.f);
-        L = L * alpha + (float)f.isum * pb;
+        L = L * alpha + (f.corr[0] * -32768.f) * pb;     // corr * -2^15 = ΣP exactly
         rref = r_new;
         // O * alpha is exact when alpha == 1 (running max unchanged): skip it when
         // that holds for every row of the wave (a wave-uniform branch)
@@ -555,15 +618,18 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 #pragma unroll
                 for (int r = 0; r < 4; r++) O[dt][r] *= alpha;
         }
-        return pb * 0.0625f;
+        return pb * 262144.f;
     };
-    // back: O^T += (V^T P^T) * vsc * pb16 per dim tile, V in buffer b.  The V
-    // operands of the next four dim tiles are read while the current four are
-    // multiplied and folded (left to itself the compiler reads each pair just before
-    // its MFMAs and waits for it: configs[4] 911 -> 891 us with the explicit prefetch).
-    auto back = [&](const v4i pop, float pb16, int b) {
+    // back: O^T += (V^T P^T) * vsc * pbv per dim tile, V in buffer b.  One A
+    // register block holds the V operands of dim tiles 2j and 2j + 1 (halves 0 and
+    // 1); the MFMA of tile 2j takes B = (P, 0), that of 2j + 1 B = (0, P), and both C
+    // = -8·ΣP·2^-18, so each result is ΣP·c·2^-18.  The V operands of the next four
+    // dim tiles are read while the current four are multiplied and folded (left to
+    // itself the compiler reads each pair just before its MFMAs and waits for it).
+    auto back = [&](const v4i pop, const v4f cc, float pbv, int b) {
         const unsigned char* vub = vu + b * VU_BYTES;
         const float* vsb = vs_l[b];
+        const v8i p_lo = cat8(pop, zero), p_hi = cat8(zero, pop);
         v4i vn[4];
 #pragma unroll
         for (int d4 = 0; d4 < 4; d4++) vn[d4] = *(reinterpret_cast<const v4i*>(vub) + d4 * 64 + lane);
@@ -576,13 +642,18 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
 #pragma unroll
                 for (int d4 = 0; d4 < 4; d4++) vn[d4] = *(reinterpret_cast<const v4i*>(vub) + (4 * dq + 4 + d4) * 64 + lane);
             }
-            const v16f ps = outer16(vsb[64 * dq + lane], pb16);   // vsc * pb16 of dim tiles 4dq..4dq+3
+            const v16f ps = outer16(vsb[64 * dq + lane], pbv);   // vsc * pbv of dim tiles 4dq..4dq+3
 #pragma unroll
-            for (int d4 = 0; d4 < 4; d4++) {
-                const int dt = 4 * dq + d4;
-                const v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vcur[d4], pop, zero, 0, 0, 0);
+            for (int d2 = 0; d2 < 4; d2 += 2) {
+                const v8i a = cat8(vcur[d2], vcur[d2 + 1]);
+                const v4f acc0 = mfma_e4m3(a, p_lo, cc);
+                const v4f acc1 = mfma_e4m3(a, p_hi, cc);
+                const int dt = 4 * dq + d2;
 #pragma unroll
-                for (int r = 0; r < 4; r++) O[dt][r] = fmaf((float)acc[r], ps[4 * d4 + r], O[dt][r]);
+                for (int r = 0; r < 4; r++) {
+                    O[dt][r] = fmaf(acc0[r], ps[4 * d2 + r], O[dt][r]);
+                    O[dt + 1][r] = fmaf(acc1[r], ps[4 * d2 + 4 + r], O[dt + 1][r]);
+                }
             }
         }
     };
@@ -605,7 +676,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         Front f = t0 >= t_mask ? front(t0, t0 & 1, std::true_type{}) : front(t0, t0 & 1, std::false_type{});
         __syncthreads();     // K buffer t0&1 is rewritten in the first iteration
         auto step = [&](int t, auto mask_tag) {
-            const float pb16 = update(f);
+            const float pbv = update(f);
             store_k(sk, t & 1, t + 2);
             store_v(sv, (t + 1) & 1, t + 1);
             load_k(sk, t + 3);
@@ -614,14 +685,15 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             // their use at the top of the next iteration, exposing their latency
             asm volatile("" ::: "memory");
             const Front fn = front(t + 1, (t + 1) & 1, mask_tag);
-            back(f.pop, pb16, t & 1);
+            back(f.pop, f.corr, pbv, t & 1);
             f = fn;
             __syncthreads();
         };
         int t = t0;
         for (; t + 1 < t1 && t + 1 < t_mask; t++) step(t, std::false_type{});
         for (; t + 1 < t1; t++) step(t, std::true_type{});
-        back(f.pop, update(f), t & 1);
+        const float pbv = update(f);
+        back(f.pop, f.corr, pbv, t & 1);
     }
     if (nsplit == 1) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
