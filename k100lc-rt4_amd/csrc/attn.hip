@@ -513,7 +513,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // the causal mask (MASK: the tile may reach past a row of this workgroup), the
     // tile max m of each row, the P codes as the PV operand and -8·ΣP·2^-18.
     struct Front {
-        v4i pop;
+        v8i p_lo, p_hi; // the P codes in the low / high half of a PV operand, zeros in the other
         float m;
         v4f corr;       // the same value in all four registers (every output row)
     };
@@ -589,13 +589,14 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             pk[kt] = __builtin_bit_cast(uint32_t, w);
         }
         Front f;
-        f.pop = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+        f.p_lo = v8i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3], 0, 0, 0, 0};
+        f.p_hi = v8i{0, 0, 0, 0, (int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
         f.m = m;
         // -8·Σ_k P·2^-18 of the row over the tile's 64 keys on the matrix pipe: A
         // bytes -2^-6 (E4M3 0x88) against the P half give it in every output row
         const v8i neg8 = {(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888,
                           (int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};
-        f.corr = mfma_e4m3(neg8, cat8(f.pop, zero), v4f{0.f, 0.f, 0.f, 0.f});
+        f.corr = mfma_e4m3(neg8, f.p_lo, v4f{0.f, 0.f, 0.f, 0.f});
         return f;
     };
     // Online update with a tile's (m, -8·ΣP·2^-18): the running reference, L, and O
@@ -626,10 +627,12 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // = -8·ΣP·2^-18, so each result is ΣP·c·2^-18.  The V operands of the next four
     // dim tiles are read while the current four are multiplied and folded (left to
     // itself the compiler reads each pair just before its MFMAs and waits for it).
-    auto back = [&](const v4i pop, const v4f cc, float pbv, int b) {
+    auto back = [&](const v8i p_lo, const v8i p_hi, const v4f cc, float pbv, int b) {
         const unsigned char* vub = vu + b * VU_BYTES;
         const float* vsb = vs_l[b];
-        const v8i p_lo = cat8(pop, zero), p_hi = cat8(zero, pop);
+        // raised issue priority over the PV block: the other wave on the SIMD then
+        // fills the matrix-core gaps with its S/P work (configs[4] 830 -> 816 us)
+        __builtin_amdgcn_s_setprio(1);
         v4i vn[4];
 #pragma unroll
         for (int d4 = 0; d4 < 4; d4++) vn[d4] = *(reinterpret_cast<const v4i*>(vub) + d4 * 64 + lane);
@@ -656,6 +659,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 }
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     if (t0 < t1) {      // uniform over the workgroup
@@ -675,8 +679,8 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         __syncthreads();
         Front f = t0 >= t_mask ? front(t0, t0 & 1, std::true_type{}) : front(t0, t0 & 1, std::false_type{});
         __syncthreads();     // K buffer t0&1 is rewritten in the first iteration
-        auto step = [&](int t, auto mask_tag) {
-            const float pbv = update(f);
+        auto step = [&](int t, const Front& fc, auto mask_tag) -> Front {
+            const float pbv = update(fc);
             store_k(sk, t & 1, t + 2);
             store_v(sv, (t + 1) & 1, t + 1);
             load_k(sk, t + 3);
@@ -685,15 +689,22 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             // their use at the top of the next iteration, exposing their latency
             asm volatile("" ::: "memory");
             const Front fn = front(t + 1, (t + 1) & 1, mask_tag);
-            back(f.pop, f.corr, pbv, t & 1);
-            f = fn;
+            back(fc.p_lo, fc.p_hi, fc.corr, pbv, t & 1);
             __syncthreads();
+            return fn;
         };
+        // Unmasked tiles two per trip: the P operands of consecutive tiles then
+        // alternate between two register sets instead of being copied every tile.
         int t = t0;
-        for (; t + 1 < t1 && t + 1 < t_mask; t++) step(t, std::false_type{});
-        for (; t + 1 < t1; t++) step(t, std::true_type{});
+        const int t_um = t1 < t_mask ? t1 : t_mask;     // unmasked steps: t + 1 < t_um
+        for (; t + 2 < t_um; t += 2) {
+            const Front g = step(t, f, std::false_type{});
+            f = step(t + 1, g, std::false_type{});
+        }
+        for (; t + 1 < t_um; t++) f = step(t, f, std::false_type{});
+        for (; t + 1 < t1; t++) f = step(t, f, std::true_type{});
         const float pbv = update(f);
-        back(f.pop, f.corr, pbv, t & 1);
+        back(f.p_lo, f.p_hi, f.corr, pbv, t & 1);
     }
     if (nsplit == 1) {
         const float inv = L > 0.f ? 1.f / L : 0.f;
