@@ -60,7 +60,10 @@
 // for O; four v_mfma_f32_4x4x1f32 cost about twice the matrix-core time of one),
 // and K/V are read with range-checked buffer loads.  The power-of-two factors of
 // the operand encodings (2^-9 for S, 2^-18 for O) are folded into the Q scale and
-// the P scale, so every rounded operation is the one the integer form had.
+// the P scale, so every rounded operation is the one the integer form had.  The
+// online rescale keeps its reference until a tile max exceeds it by more than 8
+// (log2 units): the same O / L as the reference's running-max form, rounded
+// differently, with the 64-multiply rescale of O rare instead of frequent.
 #include <type_traits>
 
 #include "rt4_dev.h"
@@ -557,7 +560,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             m = fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
         }
         // Fully masked row in this tile: take the running reference (the state after
-        // the previous tile), so alpha = 1 and every P is 2^(-inf) = 0.  (The
+        // the previous tile), so nothing is rescaled and every P is 2^(-inf) = 0.  (The
         // reference masks with -1e30 and reaches this only after a visible tile;
         // -inf gives the same P there and also keeps a row that has seen nothing
         // yet -- possible at the start of a KV split -- at zero.)
@@ -602,23 +605,31 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // Online update with a tile's (m, -8·ΣP·2^-18): the running reference, L, and O
     // rescaled by alpha.  Returns the P scale beta/7 times the 2^18 of the PV
     // operand bytes.
+    //
+    // The running reference rref moves only when a tile max exceeds it by more than
+    // 8 (log2 units) in some row of the wave; otherwise beta = 2^(m - rref) <= 2^8
+    // carries the difference.  O and L are then both 2^(max - rref) times the
+    // reference's (flash_attn_core.h, running max), so O / L and the split combine
+    // (which rescales by the stored rref) are the same quantities, rounded
+    // differently; the rescale of O (64 multiplies) runs a few times per split
+    // instead of on about a third of the tiles (configs[4] 802 -> 764 us).  With
+    // beta <= 2^8, O stays finite for V scales below about 10^28.
     auto update = [&](const Front& f) -> float {
-        const float r_new = fmaxf(rref, f.m);
-        // v_exp_f32 directly: both arguments are <= 0, and a factor below 2^-126
-        // (flushed to zero) scales contributions that no longer count
-        const float alpha = __builtin_amdgcn_exp2f(rref - r_new);
-        const float beta = __builtin_amdgcn_exp2f(f.m - r_new);
-        const float pb = beta * (1.f / 7.f);
-        L = L * alpha + (f.corr[0] * -32768.f) * pb;     // corr * -2^15 = ΣP exactly
-        rref = r_new;
-        // O * alpha is exact when alpha == 1 (running max unchanged): skip it when
-        // that holds for every row of the wave (a wave-uniform branch)
-        if (!__all(alpha == 1.f)) {
+        if (__any(f.m > rref + 8.f)) {      // a wave-uniform branch
+            const float r_new = fmaxf(rref, f.m);
+            // v_exp_f32 directly: the argument is <= 0, and a factor below 2^-126
+            // (flushed to zero) scales contributions that no longer count
+            const float alpha = __builtin_amdgcn_exp2f(rref - r_new);
+            L *= alpha;
+            rref = r_new;
 #pragma unroll
             for (int dt = 0; dt < 16; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) O[dt][r] *= alpha;
         }
+        const float beta = __builtin_amdgcn_exp2f(f.m - rref);
+        const float pb = beta * (1.f / 7.f);
+        L += (f.corr[0] * -32768.f) * pb;     // corr * -2^15 = ΣP exactly
         return pb * 262144.f;
     };
     // back: O^T += (V^T P^T) * vsc * pbv per dim tile, V in buffer b.  One A
