@@ -236,7 +236,9 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
 /* Causal int4 FlashAttention prefill, GQA (KV head = head / ratio), out f32
  * [n_heads][n_q][256] = softmax(Q K^T) V with the reference's fixed-point
  * algorithm: per 64-key tile P = clamp(int(7 exp(s - m_tile) + 0.5), 0, 7) and
- * online rescaling.  Query row i has position off + i.  Replaces the prefill
+ * online rescaling (the running reference moves only when a tile's max exceeds
+ * it by more than a factor 2^8: the same O and L, rounded differently).  Query
+ * row i has position off + i.  Replaces the prefill
  * branch of k_attention (src/kernels.h:81, src/k_fa.hip:282-300; kernel fa_int4,
  * kernels/flash_attn_core.h:74-435).  n_q % 64 == 0, kv_cap % 64 == 0,
  * n_tile * 64 <= kv_cap, kv_cap <= 16777152 (2^24 - 64: one KV head's cache is

@@ -900,12 +900,21 @@ GemvCfg gemv_mfma_cfg(int rows, int N, int K, int cus) {
     // vs the 2-group rule below): M=4 K=5120 N=17408 10.5 vs 11.2, N=10240 7.7
     // vs 8.1; K=17408 N=5120 10.9 vs 11.2, N=17408 31.8 vs 36.0; M=2 K=5120
     // N=17408 10.2 vs 10.9.  One row gains nothing measurable (C0 6.0 either way).
-    if (c.rb == 1 && rows >= 2 && NG % 4 == 0 && (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
+    // Three rows up to 2 tiles per CU (2.75 at K < 16384) take the 2-group form
+    // below: M=3 K=17408 N=5120 11.3 vs 13.8 us, N=2048 8.7 vs 10.1; K=5120 N=5120
+    // 6.8 vs 8.6, N=10240 8.5 vs 8.7; but K=17408 N=10240 18.8 here vs 20.0.
+    const bool three_wide = rows == 3 && (tpc <= 2.0 || (tpc <= 2.75 && K < 16384));
+    if (c.rb == 1 && rows >= 2 && NG % 4 == 0 && !three_wide &&
+        (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
         c.gpw = 4;
         int w = tpc <= 2.75 ? 8 : rows == 3 ? 4 : 2;
         const int nc = NG / 4;
         c.waves = w < nc ? w : nc;
-        c.max_split = 4;
+        // Leftover tiles in at most 4 K pieces above 3 tiles per CU; below that the
+        // pieces keep >= 32 groups (0): whole tiles at K=5120 (M=4 N=5120 6.6 vs
+        // 7.7 us in 4 pieces, M=2 6.3 vs 7.5, M=2 N=2048 5.2 vs 6.4), still 4
+        // pieces at K=17408.
+        c.max_split = tpc > 3.0 ? 4 : 0;
         return c;
     }
     if (c.rb == 1 && (tpc <= 5.0 || (rows >= 3 && tpc <= 7.5))) {
