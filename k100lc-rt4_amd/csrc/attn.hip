@@ -510,7 +510,6 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
     };
 
-    const v4i zero = {0, 0, 0, 0};
     const v4f cS0 = {cS[0], cS[0], cS[0], cS[0]}, cS1 = {cS[1], cS[1], cS[1], cS[1]};
     // front of tile t (K in buffer b): S^T = K Q^T for the 4 subtiles of 16 keys,
     // the causal mask (MASK: the tile may reach past a row of this workgroup), the

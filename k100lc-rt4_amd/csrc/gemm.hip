@@ -22,16 +22,14 @@
 //     facc += f32(acc) * S,   S = sa * sb,   acc = 16*I exactly (x16 nibble unpack),
 // and the result is scaled by 1/16 once at the end (a power of two, so the bits
 // equal those of scaling every term).  S is formed on the matrix core: one
-// v_mfma_f32_32x32x8_bf16 per row tile gives the rank-1 products sa (x) sb in
-// the accumulator layout.  Its operands are exact bf16 splits: sa = b1 + b2 + b3
-// (three bf16 values, 3 x 8 significant bits holding fp32's 24, made per unit by
-// the two waves that load sa, one row per lane, into LDS before the unit's
-// barrier) and sb = c1 + c2 + c3 (the same split of the fp32 weight scale; the
-// RT4 scales are fp16 values, which leave c3 = 0), so the eight products b_i *
-// c_j other than b3 * c3 (below 2^-32 of sa * sb) are exact and the MFMA's fp32
-// sum of them is sa * sb to within a few units in the last place.  The
-// bf16 MFMA occupies the matrix core ~15 cycles against ~70 for the fp32 one
-// (v_mfma_f32_32x32x2_f32 with its k = 1 half zero), measured.
+// two-block fp32 outer product (v_mfma_f32_32x32x1_2b_f32) per pair of row tiles
+// gives sa (x) sb for both in the accumulator layout of the int8 tiles (block b:
+// the activation scales of row tile 2p + b from lanes 32b..32b+31, the weight
+// scale of the lane's column in both halves).  Every element is one fp32
+// product, so S is sa * sb correctly rounded, as the reference forms it
+// (kernels/gemm_core.h:183).  Against four bf16 MFMAs on exact 3-part splits of
+// both scales (the earlier form, within a few ulp) it drops the split work of
+// every wave and one LDS pass per unit: C2 gate/up 143 -> 139 us, measured.
 //
 // What bounds this kernel on gfx950 is instruction issue: measured, a SIMD with
 // two such waves issues about one instruction per 4 cycles whatever its kind
@@ -77,23 +75,7 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef short v4h __attribute__((ext_vector_type(4)));   // four bf16 bit patterns (MFMA operand)
-
-// sb = c1 + c2 + c3, each the bf16 truncation of what is left (fp32's 24
-// significant bits in 3 x 8; an fp16-valued sb leaves c3 = 0), as the B operand of
-// the scale MFMA: (c1, c2, c3, c1) in lanes 0..31, (c2, c3, c1, c2) in lanes
-// 32..63.  Against the A operand (b1, b1, b1, b2 | b2, b2, b3, b3) of sa's split the
-// MFMA sums every product b_i c_j except b3 c3 (below 2^-32 of sa*sb).  lhm: all
-// ones in lanes 32..63 (bitwise selects: a select on the lane half compiled to a
-// branch).
-__device__ __forceinline__ v4h split_sb(float sb, uint32_t lhm) {
-    const uint32_t c1 = __float_as_uint(sb) & 0xFFFF0000u;
-    const float r1 = sb - __uint_as_float(c1);
-    const uint32_t c2 = __float_as_uint(r1) & 0xFFFF0000u;
-    const uint32_t c3 = __float_as_uint(r1 - __uint_as_float(c2)) & 0xFFFF0000u;
-    const uint32_t p12 = (c1 >> 16) | c2, p31 = (c3 >> 16) | c1, p23 = (c2 >> 16) | c3;
-    return __builtin_bit_cast(v4h, make_uint2((p23 & lhm) | (p12 & ~lhm), (p12 & lhm) | (p31 & ~lhm)));
-}
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int BM = 128;           // activation rows per tile
 constexpr int BN = 256;           // weight rows (output columns) per tile
@@ -101,8 +83,7 @@ constexpr int NT = 512;           // 8 waves
 constexpr int NS = 4;             // LDS stages
 constexpr int A_ST = BM * 128;    // int8 activation tile per stage
 constexpr int B_ST = BN * 64;     // packed weight tile per stage
-constexpr int S_ST = 4096;        // sa (512 B) + sb (1024 B) + 512 B written by the two idle waves + sa splits (2048 B)
-constexpr int S_SPLIT = 2048;     // offset of the sa splits in a scale stage
+constexpr int S_ST = 2048;        // sa (512 B) + sb (1024 B) + 512 B written by the two idle waves
 constexpr int LDS_B = 0;                       // weight stages
 constexpr int LDS_A = LDS_B + NS * B_ST;       // activation stages
 constexpr int LDS_S = LDS_A + NS * A_ST;       // scale stages
@@ -186,8 +167,7 @@ __device__ __forceinline__ void add4_dev16(v16i& f, const float* p) {
 //   B  [256 rows][4 x 16 B] packed, chunk c of row r stored at c ^ ((r >> 2) & 3);
 //      wave w loads rows 32w..32w+31, the ones it reads
 //   S  sa[128] f32 (waves 0, 1), sb[256] f32 (waves 2..5); waves 6, 7 repeat an sb
-//      load into the spare 512 B so that every wave issues the same count; then
-//      the bf16 splits of sa, [128 rows][16 B] at S_SPLIT, written by waves 0, 1.
+//      load into the spare 512 B so that every wave issues the same count.
 struct DmaOff {
     uint32_t a[2], b[2], s;
 };
@@ -239,7 +219,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     const int lane = threadIdx.x & 63;
     const int w = uniform(threadIdx.x >> 6);
     const int lr = lane & 31, lh = lane >> 5;
-    const uint32_t lhm = 0u - (uint32_t)lh;   // all ones in lanes 32..63
     const int NG = K >> 7;
     const int P = gridDim.x;
     const int b = (P % 8 == 0) ? (int)(blockIdx.x % 8) * (P / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
@@ -258,7 +237,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const int r = 32 * w + lr;
         rb[s2] = LDS_B + r * 64 + (((2 * s2 + lh) ^ ((r >> 2) & 3)) * 16);
     }
-    int rsa = LDS_S + S_SPLIT + lr * 16 + lh * 8, rsb = LDS_S + 512 + (32 * w + lr) * 4;
+    // sa of row 64p + lane (row tile 2p in lanes 0..31, 2p + 1 in lanes 32..63) at
+    // rsa + 256p; sb of this lane's column at rsb
+    int rsa = LDS_S + lane * 4, rsb = LDS_S + 512 + (32 * w + lr) * 4;
     // per-wave LDS destinations of the DMA (m0 = base + stage immediate)
     const uint32_t L = lds_addr(lds);
     const uint32_t dstA = L + LDS_A + 2 * w * 1024, dstB = L + LDS_B + 2 * w * 1024;
@@ -273,25 +254,25 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         for (int r = 0; r < 16; r++) facc[i][r] = 0;
 
     const v16i zero16 = {};
-    const v16f zero16f = {};
+    const v32f zero32f = {};
     auto unpack_ks = [&](v4i (&bu_)[4], const uint4 (&bp_)[2], int ks) {
         const uint4 p = bp_[ks >> 1];
         const uint32_t x0 = (ks & 1) ? p.z : p.x, x1 = (ks & 1) ? p.w : p.y;
         bu_[ks] = v4i{(int)even_x16(x0), (int)odd_x16(x0), (int)even_x16(x1), (int)odd_x16(x1)};
     };
-    // Scale products of row tile ii on the matrix core: v_mfma_f32_32x32x8_bf16 (lane
-    // l supplies row / column l & 31 at k = 4(l >> 5) .. +3) with
-    //   A: lanes 0..31 (b1, b1, b1, b2), lanes 32..63 (b2, b2, b3, b3)  of sa's split,
-    //   B: lanes 0..31 (c1, c2, c3, c1), lanes 32..63 (c2, c3, c1, c2)  of sb's split,
-    // gives S[r] = sum of b_i c_j over (i, j) != (3, 3) = sa[row of register r] *
-    // sb[this lane's column] in the accumulator layout of the int8 tiles.  A row's
-    // split record holds the two dword pairs in that order, so lane (lr, lh) reads
-    // its pair at 8 * lh.
-    auto sa_of = [&](int ii) __attribute__((always_inline)) -> v4h {
-        return *reinterpret_cast<const v4h*>(lds + rsa + ii * 512);
+    // Scale products of row tiles 2p and 2p + 1: the two-block outer product
+    // (v_mfma_f32_32x32x1_2b_f32; block b takes its rows from lanes 32b..32b+31 and
+    // its columns from the same lanes) of sa[64p + lane] and sb[this lane's column]
+    // puts sa[row of register r] * sb[column] of tile 2p + b in register 16b + r,
+    // the accumulator layout of the int8 tiles.
+    auto scales2 = [&](float sa_pair, float sb_col) __attribute__((always_inline)) -> v32f {
+        return __builtin_amdgcn_mfma_f32_32x32x1f32(sa_pair, sb_col, zero32f, 0, 0, 0);
     };
-    auto scales = [&](v4h sa_split, v4h sb_split) __attribute__((always_inline)) -> v16f {
-        return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sa_split, sb_split, zero16f, 0, 0, 0);
+    auto slo = [](const v32f& v) __attribute__((always_inline)) -> v16f {
+        return __builtin_shufflevector(v, v, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+    };
+    auto shi = [](const v32f& v) __attribute__((always_inline)) -> v16f {
+        return __builtin_shufflevector(v, v, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
     };
     // quarter q of the fold of row tile ii (registers 4q..4q+3)
     auto fold_q = [&](v16i& fa, const v16i& acc, const v16f& S, int ii, int q, const TileRef& x) __attribute__((always_inline)) {
@@ -420,19 +401,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     const void* sbase = (w < 2 ? (const void*)sa : (const void*)sb);
     const uint32_t s_step = (w < 2 ? (uint32_t)M : (uint32_t)N) * 4u;
     DmaOff off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
-    off.a[0] += dg0 * 128;
-    off.a[1] += dg0 * 128;
-    off.b[0] += dg0 * 64;
-    off.b[1] += dg0 * 64;
-    off.s += dg0 * s_step;
+    // the group moves the (scalar) source bases; the per-lane offsets change per tile
+    const char* bA = reinterpret_cast<const char*>(A) + (size_t)dg0 * 128;
+    const char* bW = reinterpret_cast<const char*>(W) + (size_t)dg0 * 64;
+    const char* bS = reinterpret_cast<const char*>(sbase) + (size_t)dg0 * s_step;
     // DMA of the unit at the DMA side's position into stage st
     auto issue = [&](int st) __attribute__((always_inline)) {
         const uint32_t da = dstA + st * A_ST, db = dstB + st * B_ST, ds = dstS + st * S_ST;
-        dma16<0>(off.a[0], A, da);
-        dma16<1024>(off.a[1], A, da);
-        dma16<0>(off.b[0], W, db);
-        dma16<1024>(off.b[1], W, db);
-        dma4<0>(off.s, sbase, ds);
+        dma16<0>(off.a[0], bA, da);
+        dma16<1024>(off.a[1], bA, da);
+        dma16<0>(off.b[0], bW, db);
+        dma16<1024>(off.b[1], bW, db);
+        dma4<0>(off.s, bS, ds);
     };
     auto advance_dma = [&]() __attribute__((always_inline)) {
         if (--dleft == 0) {
@@ -442,12 +422,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
                 ++dtn;
             }
             off = dma_offsets(dtm * BM, dtn * BN, M, N, K, w, lane);
+            bA = reinterpret_cast<const char*>(A);
+            bW = reinterpret_cast<const char*>(W);
+            bS = reinterpret_cast<const char*>(sbase);
         } else {
-            off.a[0] += 128;
-            off.a[1] += 128;
-            off.b[0] += 64;
-            off.b[1] += 64;
-            off.s += s_step;
+            bA += 128;
+            bW += 64;
+            bS += s_step;
         }
     };
 
@@ -462,18 +443,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         cur.bn = tn * BN;
     }
 
-    // The bf16 splits of a stage's activation scales (split_scale_bf16x3), one row
-    // per lane of waves 0 and 1, which load those scales: called after their wait
-    // for that stage's DMA and before the barrier that orders these LDS writes
-    // before every wave's reads.
-    auto split_stage = [&](int stn) __attribute__((always_inline)) {
-        if (w < 2) {
-            unsigned char* b = lds + LDS_S + stn * S_ST;
-            const float sv = *reinterpret_cast<const float*>(b + (64 * w + lane) * 4);
-            *reinterpret_cast<uint4*>(b + S_SPLIT + (64 * w + lane) * 16) = split_scale_bf16x3(sv);
-        }
-    };
-
     // prologue: DMA of units 0..3, then the fragments of unit 0
     issue(0);
     if (n > 1) { advance_dma(); issue(1); }
@@ -481,21 +450,23 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     if (n > 3) { advance_dma(); issue(3); }
     if (n > 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * DMA_PER_UNIT) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    split_stage(0);
     __syncthreads();
     v4i a_cur[4], a_nxt[4], bu[4];
     uint4 bp[2];
     // fragment reads: per-lane offsets into the current stage (moved on by one stage
-    // per unit: one add per register) plus the row tile (an immediate)
+    // per unit: one add per register) plus the row tile (an immediate).  The adds
+    // are asm with the register tied in place: written in C, the compiler kept the
+    // old and the new offsets alive together and spent 17 adds and 4 moves per
+    // unit on the 8 updates (C2 gate/up 139 -> 138 us with them in place).
     auto next_stage = [&](int st_next) __attribute__((always_inline)) {
         const int da = st_next ? A_ST : -(NS - 1) * A_ST, db = st_next ? B_ST : -(NS - 1) * B_ST;
         const int ds = st_next ? S_ST : -(NS - 1) * S_ST;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) ra[ks] += da;
+        for (int ks = 0; ks < 4; ks++) asm volatile("v_add_u32 %0, %1, %0" : "+v"(ra[ks]) : "s"(da));
 #pragma unroll
-        for (int s2 = 0; s2 < 2; s2++) rb[s2] += db;
-        rsa += ds;
-        rsb += ds;
+        for (int s2 = 0; s2 < 2; s2++) asm volatile("v_add_u32 %0, %1, %0" : "+v"(rb[s2]) : "s"(db));
+        asm volatile("v_add_u32 %0, %1, %0" : "+v"(rsa) : "s"(ds));
+        asm volatile("v_add_u32 %0, %1, %0" : "+v"(rsb) : "s"(ds));
     };
     auto read_a = [&](v4i (&dst)[4], int ii) __attribute__((always_inline)) {
 #pragma unroll
@@ -506,14 +477,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         for (int s2 = 0; s2 < 2; s2++) bp[s2] = *reinterpret_cast<const uint4*>(lds + rb[s2]);
     };
     // the scale operands of a unit, read once its stage is valid (right after the
-    // barrier that follows its split) so the scale MFMAs never wait for a fresh LDS
-    // read: sb of this wave's column and the sa splits of the four row tiles
-    v4h sap[4];
+    // unit's barrier): sb of this wave's column and sa of the two row-tile pairs
+    float sa2[2];
     float sbr;
     auto read_s = [&]() __attribute__((always_inline)) {
         sbr = *reinterpret_cast<const float*>(lds + rsb);
-#pragma unroll
-        for (int ii = 0; ii < 4; ii++) sap[ii] = sa_of(ii);
+        sa2[0] = *reinterpret_cast<const float*>(lds + rsa);
+        sa2[1] = *reinterpret_cast<const float*>(lds + rsa + 256);
     };
     read_a(a_cur, 0);
     read_b();
@@ -526,7 +496,10 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
     // Accumulators with fixed roles: row tiles 0 and 2 of a unit go to accA, tiles
     // 1 and 3 to accB, and a fold reads the one the MFMAs are not writing (no copies).
     v16i accA, accB;
-    v16f Se, So;         // scale products of the even and odd row tiles
+    // Scale products: one buffer of two row tiles, (0, 1) from after row tile 0's
+    // MFMAs (until then it holds tiles 2 and 3 of the previous unit, the last of which
+    // is folded during row tile 0), (2, 3) from before the unit's barrier.
+    v32f S2;
     // One row-tile step: the four MFMAs of tile (a, bu) into acc, each followed by a
     // quarter of the fold of the previous tile (prev into facc[fi], with its scale
     // products S, formed one row tile earlier) and, with UNPACK, by the unpack of
@@ -554,23 +527,16 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // row tile 0, with the unpack of this unit's weights and the fold of the
         // previous unit's last tile
         read_a(a_nxt, 1);
-        const v4h sbz = split_sb(sbr, lhm);
-        // The scale products of each row tile are formed before its MFMAs, in the
-        // buffer of its parity (even tiles Se, odd So), so they are ready long
-        // before the tile is folded during the next row tile (configs[2]: ~1-2%
-        // against forming them after the MFMAs and starting the fold one MFMA late).
-        // (for the first unit of a segment accB is zero: the fold adds exact zeros)
-        Se = scales(sap[0], sbz);
-        step(a_cur, accA, accB, facc[3], 3, xprev, true, So);
-        So = scales(sap[1], sbz);
+        // (for the first unit of a segment accB and S2 are zero: the fold adds exact zeros)
+        step(a_cur, accA, accB, facc[3], 3, xprev, true, shi(S2));
+        S2 = scales2(sa2[0], sbr);
         // row tile 1, fold of tile 0
         read_a(a_cur, 2);
-        step(a_nxt, accB, accA, facc[0], 0, x, false, Se);
-        Se = scales(sap[2], sbz);
+        step(a_nxt, accB, accA, facc[0], 0, x, false, slo(S2));
         // row tile 2, fold of tile 1
         read_a(a_nxt, 3);
-        step(a_cur, accA, accB, facc[1], 1, x, false, So);
-        So = scales(sap[3], sbz);   // before the barrier: sap is refilled with the next unit's after it
+        step(a_cur, accA, accB, facc[1], 1, x, false, shi(S2));
+        S2 = scales2(sa2[1], sbr);   // before the barrier: sa2, sbr are refilled with the next unit's after it
         // row tile 3.  The DMA of unit i+1 has landed once at most the two younger
         // units' loads are pending (three units in flight), and every wave has issued
         // its last read of this stage (the barrier waits for LDS reads).  Near the
@@ -580,7 +546,6 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         // variant stores as it goes.  In those cases no count bound is safe: drain.
         if (GSUM || first || i + 3 >= n) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_UNIT) : "memory");
-        split_stage((st + 1) & (NS - 1));   // unit i+1's scales (stale past the share's end: unread)
         __syncthreads();
         if (i + 4 < n) {
             advance_dma();
@@ -590,7 +555,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         read_b();
         read_a(a_cur, 0);
         read_s();
-        step(a_nxt, accB, accA, facc[2], 2, x, false, Se);
+        step(a_nxt, accB, accA, facc[2], 2, x, false, slo(S2));
         ++i;
         if (GSUM) ++cur.g;
     };
@@ -600,13 +565,13 @@ __global__ __launch_bounds__(NT, 1) void gemm_w4a8_k(const int8_t* __restrict__ 
         const int len = min(NG - g0, n - i);
         if (GSUM) cur.g = g0;
         accB = zero16;
-        So = zero16f;
+        S2 = zero32f;
         for (int k = 0; k < len; k++) unit(k == 0);
         // the segment's last row tile 3, then publish the segment
         TileRef xl = cur;
         if (GSUM) xl.g = cur.g - 1;
 #pragma unroll
-        for (int q = 0; q < 4; q++) fold_q(facc[3], accB, So, 3, q, xl);
+        for (int q = 0; q < 4; q++) fold_q(facc[3], accB, shi(S2), 3, q, xl);
         flush(cur);
         // the next unit's fragments, read again from its stage (still intact): the
         // copies read during the last unit are then dead across the flush, which

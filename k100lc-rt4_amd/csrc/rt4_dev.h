@@ -82,19 +82,4 @@ __device__ __forceinline__ float load_dev(const float* p) {
     return v;
 }
 
-// An fp32 activation scale split into three bf16 values b1 + b2 + b3 = s (each the
-// bf16 truncation of what is left, so both subtractions are exact and fp32's 24
-// significant bits fit in 3 x 8), packed as the prefill GEMM's scale-MFMA A operand
-// (k = 0..3 in lanes 0..31, k = 4..7 in lanes 32..63): {b1:b1, b1:b2 | b2:b2, b3:b3}
-// as bf16 pairs (low half first).  Exact for every finite s at or above 2^-110
-// (below that the last part can fall into fp32's subnormal range); an infinite s
-// gives NaN parts.
-__device__ __forceinline__ uint4 split_scale_bf16x3(float s) {
-    const uint32_t b1 = __float_as_uint(s) & 0xFFFF0000u;
-    const float r1 = s - __uint_as_float(b1);
-    const uint32_t b2 = __float_as_uint(r1) & 0xFFFF0000u;
-    const uint32_t b3 = __float_as_uint(r1 - __uint_as_float(b2)) & 0xFFFF0000u;
-    return make_uint4(b1 | (b1 >> 16), b2 | (b1 >> 16), b2 | (b2 >> 16), b3 | (b3 >> 16));
-}
-
 }  // namespace rt4

@@ -190,12 +190,45 @@ def test_gemm_tail_tiles_with_continuing_workgroups(rt4, orc, torch_gpu, entry, 
     assert err < TIGHT and worst < 1e-5
 
 
+@pytest.mark.parametrize("entry", ["i8", "w4a4"])
+def test_gemm_single_group_matches_fp32_fold_bitwise(rt4, orc, torch_gpu, entry):
+    """One 128-wide group (K = 128): every tile is a single unit, so C is one fold
+    step.  The reference folds acc = fmaf((float)I, SA*SB, acc) from acc = 0
+    (kernels/gemm_core.h:176-183), i.e. f32(I) * f32(sa * sb) with one rounding of
+    each product.  The kernel forms sa*sb as one fp32 product on the matrix core
+    and folds 16*I (exact), scaled by 1/16 at the end (exact), so its output must
+    carry exactly those bits -- for the int8 entry and for the W4A4 one, whose
+    fold is literally the reference's gemm_w4a4."""
+    M, N, K = 256, 512, 128
+    print(f"case gemm single group entry={entry} M={M} N={N} K={K}", flush=True)
+    c, wq, ws, x = _case(torch_gpu, 53, M, N, K)
+    sb = rt4.make_group_major(ws, K)
+    if entry == "i8":
+        xq, sa = rt4.quant_rows_i8(x)
+        out = rt4.gemm_w4a8_i8(wq, sb, xq, sa)
+        q, sa_o = orc.quant_rows_i8(c["x"], M, K)
+    else:
+        aq, sa = rt4.quant_rows_a4(x)
+        out = rt4.gemm_w4a4(wq, sb, aq, sa)
+        aq_o, sa_o = orc.quant_rows_a4(c["x"], M, K, 128)
+        q = layout.unpack_rt4(aq_o).astype(np.int8)
+    torch_gpu.cuda.synchronize()
+    sb_o = orc.make_group_major(c["ws"])
+    I = orc.gemv_groupsums(c["wq"], q)[:, :, 0]
+    S = sa_o[0][:, None] * sb_o[0][None, :]                  # fp32 products, round to nearest
+    want = I.astype(np.float32) * S
+    got = host(out)
+    diff = int(np.count_nonzero(got.view(np.uint32) != want.view(np.uint32)))
+    print(f"  outputs differing from f32(I) * f32(sa * sb): {diff} of {M * N}")
+    assert diff == 0
+
+
 def test_gemm_scale_products_over_wide_exponent_range(rt4, orc, torch_gpu):
-    """The scale products sa*sb come from exact bf16 splits of both scales (three
-    parts of sa, two of the fp16-valued sb).  Activation scales spanning 2^-40 ..
-    2^40 across rows and groups exercise every exponent the splits see; each row
-    must match the fp64 oracle to fp32 accuracy on its own (a per-row relative L2,
-    so small rows are not hidden behind large ones), for both entries."""
+    """The scale products sa*sb are single fp32 products on the matrix core.
+    Activation scales spanning 2^-40 .. 2^40 across rows and groups exercise a wide
+    range of exponents; each row must match the fp64 oracle to fp32 accuracy on its
+    own (a per-row relative L2, so small rows are not hidden behind large ones), for
+    both entries."""
     M, N, K = 256, 320, 1024
     print(f"case gemm scale range M={M} N={N} K={K}", flush=True)
     c = workload.gemm_case(41, M, N, K)
