@@ -595,10 +595,16 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         f.p_hi = v8i{0, 0, 0, 0, (int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
         f.m = m;
         // -8·Σ_k P·2^-18 of the row over the tile's 64 keys on the matrix pipe: A
-        // bytes -2^-6 (E4M3 0x88) against the P half give it in every output row
-        const v8i neg8 = {(int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888,
-                          (int)0x88888888, (int)0x88888888, (int)0x88888888, (int)0x88888888};
-        f.corr = mfma_e4m3(neg8, f.p_lo, v4f{0.f, 0.f, 0.f, 0.f});
+        // bytes -2^-6 (E4M3 0x88) against the P bytes give it in every output row.
+        // Two chained 16x16x32 FP8 MFMAs over the code dwords as they are (a lane's
+        // column is its query row, as in the PV operand): their 2-register constant
+        // operand is kept, where the 8-register one of a 16x16x128 MFMA was rebuilt
+        // with moves every tile.  Every product and partial sum is exact.
+        const long neg2 = (long)0x8888888888888888ull;
+        const v4f c01 = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(
+            neg2, (long)(((uint64_t)pk[1] << 32) | pk[0]), v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        f.corr = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(neg2, (long)(((uint64_t)pk[3] << 32) | pk[2]), c01,
+                                                            0, 0, 0);
         return f;
     };
     // Online update with a tile's (m, -8·ΣP·2^-18): the running reference, L, and O
