@@ -85,6 +85,22 @@ int rt4_release_scratch(void);
 int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K,
                      void* stream);
 
+/* Per-row activation quantizer: one scale per row (G = K).  No counterpart in
+ * the reference, which quantizes per (row, 128-group); it is an opt-in mode for
+ * callers that want activations "quantized per row", as the benchmark configs
+ * describe them.  The row's scale is written into every 128-group slot of the
+ * per-group layout, so the GEMV and GEMM entries consume it unchanged.
+ *   mode 0, the GEMV form: s = amax/127 (1 for an all-zero row), codes
+ *     clamp(lrintf(x/s), -128, 127), xq int8 [rows][K] interleaved as
+ *     rt4_quant_act_a8 writes it, sa f32 [rows][K/128], asu (optional, may be
+ *     NULL) int32 [rows][K/128] = Σq per group; for rt4_gemv_w4a8_q.
+ *   mode 1, the GEMM form: s = amax/119, codes clamp(..., -128, 119), xq as
+ *     rt4_quant_rows_i8 writes it, sa f32 [K/128][rows] group-major; for
+ *     rt4_gemm_w4a8_i8.
+ * K % 128 == 0; x rows of K floats, contiguous. */
+int rt4_quant_act_rowwise(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K, int mode,
+                          void* stream);
+
 /* W4A8 GEMV on pre-quantized activations.  Replaces the gemv_w4a8<M,SMEM,NROW>
  * launch of k_gemv_w4a8 (kernels/gemv_w4a8_core.h:76-209, src/k_gemv.hip:96-103).
  * y f32 [rows][N] = Σ_g f16(ws[n][g]) * sa[m][g] * Σ_{k∈g} code[n][k]*xq[m][k].

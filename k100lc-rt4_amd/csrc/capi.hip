@@ -379,6 +379,18 @@ int rt4_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int ro
                       "rt4_quant_act_a8 launch");
 }
 
+int rt4_quant_act_rowwise(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K, int mode,
+                          void* stream) {
+    if (!xq || !sa || !x) return fail(RT4_E_ARG, "rt4_quant_act_rowwise: null pointer");
+    if (mode != 0 && mode != 1) return fail(RT4_E_ARG, "rt4_quant_act_rowwise: mode=%d (0: GEMV form, 1: GEMM form)", mode);
+    if (rows < 1) return fail(RT4_E_SHAPE, "rt4_quant_act_rowwise: rows=%d", rows);
+    if (K <= 0 || K % 128) return fail(RT4_E_SHAPE, "rt4_quant_act_rowwise: K=%d is not a positive multiple of 128", K);
+    if (!aligned(xq, 8) || !aligned(x, 4) || !aligned(sa, 4) || !aligned(asu, 4))
+        return fail(RT4_E_ARG, "rt4_quant_act_rowwise: misaligned pointer (xq needs 8 bytes)");
+    return hip_status(rt4::launch_quant_row(xq, sa, asu, x, rows, K, mode, as_stream(stream)),
+                      "rt4_quant_act_rowwise launch");
+}
+
 int rt4_gemv_w4a8_q_cfg(float* y, const uint32_t* wq, const uint16_t* ws, const int8_t* xq,
                         const float* sa, int rows, int N, int K, int groups_per_wave, int waves,
                         int k_splits, int row_blocks, void* stream) {

@@ -99,6 +99,77 @@ hipError_t launch_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float*
 }
 
 // ---------------------------------------------------------------------------
+// Per-row activation quantizer (G = K: one scale per row).  An opt-in mode with no
+// counterpart in the reference, which quantizes per (row, 128-group): the steps of
+// quant_act_a8_k (DIV 127, codes in [-128, 127]) or of quant_rows_a8_k's int8 form
+// (DIV 119, codes in [-128, 119]) with the row's max-abs, and the row's scale
+// written into every 128-group slot of the per-group layout, so that the GEMV and
+// the GEMM consume it unchanged (their fold multiplies s by the group's weight
+// scale).  One workgroup per row: a pass over the row for its max-abs (a block
+// reduction), then the quantization pass over the now cached row.  A lane handles
+// 8-element blocks i = threadIdx.x + 256 j; K % 128 == 0 keeps the 16 blocks of a
+// group on 16 consecutive lanes of one pass, all active or all not.
+// GROUP_MAJOR: scales [K/128][rows] (the GEMM's), else [rows][K/128] (the GEMV's);
+// asu (optional, [rows][K/128]): Σq per group.  grid (rows), block 256.
+template <int DIV, bool ALIGNED, bool GROUP_MAJOR>
+__global__ __launch_bounds__(256) void quant_row_k(const float* __restrict__ x, int8_t* __restrict__ xq,
+                                                   float* __restrict__ sa, int32_t* __restrict__ asu, int rows,
+                                                   int K) {
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const float* xr = x + (size_t)m * K;
+    const int nb = K >> 3;
+    float amax = 0.f;
+    for (int i = threadIdx.x; i < nb; i += 256) {
+        float v[8];
+        load8(xr + 8 * (size_t)i, ALIGNED, v);
+#pragma unroll
+        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = run_max<64>(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = amax > 0.f ? amax / (float)DIV : 1.f;
+    const bool by_recip = recip_div_ok(s);   // the same for the whole row
+    const float y = 1.f / s;
+    const int NG = K >> 7;
+    for (int i = threadIdx.x; i < nb; i += 256) {
+        float v[8];
+        load8(xr + 8 * (size_t)i, ALIGNED, v);
+        int c[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            c[e] = clampi((int)lrintf(by_recip ? div_by_recip(v[e], s, y) : v[e] / s), -128, DIV == 127 ? 127 : 119);
+        *reinterpret_cast<uint2*>(xq + (size_t)m * K + 8 * (size_t)i) = interleave8(c);
+        const int g = i >> 4;
+        if ((i & 15) == 0) sa[GROUP_MAJOR ? (size_t)g * rows + m : (size_t)m * NG + g] = s;
+        if (asu) {
+            int part = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) part += c[e];
+            part = run_sum<16>(part);
+            if ((i & 15) == 0) asu[(size_t)m * NG + g] = part;
+        }
+    }
+}
+
+hipError_t launch_quant_row(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K, int mode,
+                            hipStream_t st) {
+    const bool aligned = ((uintptr_t)x & 15) == 0;
+    const dim3 grid(rows);
+    if (mode == 0 && aligned)
+        hipLaunchKernelGGL((quant_row_k<127, true, false>), grid, dim3(256), 0, st, x, xq, sa, asu, rows, K);
+    else if (mode == 0)
+        hipLaunchKernelGGL((quant_row_k<127, false, false>), grid, dim3(256), 0, st, x, xq, sa, asu, rows, K);
+    else if (aligned)
+        hipLaunchKernelGGL((quant_row_k<119, true, true>), grid, dim3(256), 0, st, x, xq, sa, asu, rows, K);
+    else
+        hipLaunchKernelGGL((quant_row_k<119, false, true>), grid, dim3(256), 0, st, x, xq, sa, asu, rows, K);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // Prefill-side quantizer (restates quant_rows_a8_k, src/k_new.hip:268-301):
 // per (row, G-group) s = amax>0 ? amax/119 : 1, q8 = clamp(lrintf(x/s), -128, 119),
 // h = (q8+8)>>4, l = q8-16h.  Outputs the reference's layout: qh, ql u32

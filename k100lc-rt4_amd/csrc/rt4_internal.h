@@ -14,6 +14,8 @@ int set_error(int code, const char* msg);
 hipError_t launch_quant_act_a8(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows,
                                int K, hipStream_t st);
 bool quant_group_supported(int G);
+hipError_t launch_quant_row(int8_t* xq, float* sa, int32_t* asu, const float* x, int rows, int K, int mode,
+                            hipStream_t st);
 hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, int8_t* xq,
                                 const float* x, int rows, int K, int G, int in_stride, int in_off,
                                 hipStream_t st);

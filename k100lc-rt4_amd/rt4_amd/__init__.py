@@ -28,7 +28,7 @@ GROUP = 128
 # Every symbol include/rt4k.h declares (checked by the CPU test suite).
 C_EXPORTS = (
     "rt4_last_error", "rt4_abi_version", "rt4_release_scratch",
-    "rt4_quant_act_a8", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
+    "rt4_quant_act_a8", "rt4_quant_act_rowwise", "rt4_gemv_w4a8_q", "rt4_gemv_w4a8_q_cfg", "rt4_gemv_launch_plan",
     "rt4_gemv_w4a8_groupsums",
     "rt4_gemv_w4a8", "rt4_gemv_w4a8_noalloc", "rt4_gemv_w4a8_cfg", "rt4_quant_rows_a8", "rt4_quant_rows_i8", "rt4_digits_to_i8",
     "rt4_make_group_major", "rt4_quant_rows_a4", "rt4_quant_act_a4", "rt4_gemv_w4a4_q", "rt4_gemv_w4a4_q_cfg", "rt4_gemv_w4a4",
@@ -63,6 +63,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGS = {
     "rt4_quant_act_a8": [_P, _P, _P, _P, _I, _I, _P],
+    "rt4_quant_act_rowwise": [_P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_quant_act_a4": [_P, _P, _P, _I, _I, _P],
     "rt4_gemv_w4a4_q": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "rt4_gemv_w4a4_q_cfg": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
@@ -169,6 +170,20 @@ def quant_act_a8(x, want_sums: bool = False):
     sa = _empty((rows, K // GROUP), torch.float32, x.device)
     asu = _empty((rows, K // GROUP), torch.int32, x.device) if want_sums else None
     _check(lib().rt4_quant_act_a8(_ptr(xq), _ptr(sa), _ptr(asu), _ptr(x), rows, K, _stream()))
+    return (xq, sa, asu) if want_sums else (xq, sa)
+
+
+def quant_act_rowwise(x, mode: int = 0, want_sums: bool = False):
+    """Per-row quantizer (one scale per row; no counterpart in the reference).
+    mode 0: (xq int8 [rows, K] interleaved, sa f32 [rows, K/128][, asu]) for
+    gemv_w4a8_q; mode 1: (xq, sc f32 [K/128, rows]) for gemm_w4a8_i8.  The row's
+    scale fills every group slot."""
+    torch = _torch()
+    rows, K = x.shape
+    xq = _empty((rows, K), torch.int8, x.device)
+    sa = _empty((rows, K // GROUP) if mode == 0 else (K // GROUP, rows), torch.float32, x.device)
+    asu = _empty((rows, K // GROUP), torch.int32, x.device) if want_sums else None
+    _check(lib().rt4_quant_act_rowwise(_ptr(xq), _ptr(sa), _ptr(asu), _ptr(x), rows, K, mode, _stream()))
     return (xq, sa, asu) if want_sums else (xq, sa)
 
 

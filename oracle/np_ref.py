@@ -46,13 +46,16 @@ def _group_amax(x: np.ndarray, G: int) -> np.ndarray:
     return np.abs(x.reshape(M, K // G, G)).max(axis=2)
 
 
-def quant_act(x: np.ndarray):
-    """Decode-side quantizer (kernels/gemv_w4a8_core.h:34-66), vectorised."""
+def quant_act(x: np.ndarray, G: int = GROUP):
+    """Decode-side quantizer (kernels/gemv_w4a8_core.h:34-66), vectorised, per (row,
+    G).  The reference's G is 128; G = K is the per-row mode (one scale per row),
+    which has no reference counterpart: its scale s[:, 0] is the row's scale and Σq
+    is still returned per 128-group, the layouts the library writes."""
     x = np.asarray(x, np.float32)
     M, K = x.shape
-    amax = _group_amax(x, GROUP)
+    amax = _group_amax(x, G)
     s = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
-    q = np.rint(x.reshape(M, K // GROUP, GROUP) / s[:, :, None])
+    q = np.rint(x.reshape(M, K // G, G) / s[:, :, None])
     q = np.clip(q, -128, 127).astype(np.int8).reshape(M, K)
     asu = q.reshape(M, K // GROUP, GROUP).astype(np.int32).sum(axis=2)
     return q, s, asu

@@ -74,6 +74,10 @@ def test_gemv_null_and_config_errors(rt4):
 def test_quant_errors(rt4):
     L = rt4.lib()
     assert L.rt4_quant_act_a8(DUMMY, DUMMY, None, DUMMY, 1, 100, None) == 1
+    assert L.rt4_quant_act_rowwise(DUMMY, DUMMY, None, DUMMY, 1, 100, 0, None) == 1
+    assert L.rt4_quant_act_rowwise(DUMMY, DUMMY, None, DUMMY, 0, 256, 0, None) == 1
+    assert L.rt4_quant_act_rowwise(DUMMY, DUMMY, None, DUMMY, 1, 256, 2, None) == 2
+    assert "mode=2" in L.rt4_last_error().decode()
     assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 4, 256, 96, 0, 0, None) == 2
     assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 4, 200, 128, 0, 0, None) == 2
     assert L.rt4_quant_rows_a8(DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 256, 128, 0, 0, None) == 1
