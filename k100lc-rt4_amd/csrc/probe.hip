@@ -28,12 +28,13 @@
 //                   FP4 operands (the matrix-core rate per format)
 //   rt4p_gemm_unit  the prefill GEMM's per-unit instruction skeleton without memory:
 //                   per wave and 128-wide K group, four 32x32 row tiles of MFMAs with
-//                   the previous row tile's fold interleaved and the bf16 scale
-//                   products, at the GEMM's occupancy (8 waves per CU); variant 0 the
-//                   int8 form (16 v_mfma_i32_32x32x32_i8, fold cvt + fma), variant 1
-//                   an exact FP8-digit form (16 v_mfma_scale_f32_32x32x64_f8f6f4 over
-//                   two digit planes, fold one fma, a bias and a scale bf16 MFMA per
-//                   row tile)
+//                   the previous row tile's fold interleaved, at the GEMM's occupancy
+//                   (8 waves per CU); variant 0 the product's int8 form (16
+//                   v_mfma_i32_32x32x32_i8, fold cvt + fma, the scale products as two
+//                   two-block fp32 outer products per unit placed as in the GEMM),
+//                   variant 1 an exact FP8-digit form (16
+//                   v_mfma_scale_f32_32x32x64_f8f6f4 over two digit planes, fold one
+//                   fma, a bias and a scale bf16 MFMA per row tile)
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
@@ -45,6 +46,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 typedef short v4h __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void hbm_read_k(const uint4* __restrict__ src, size_t n16,
@@ -379,6 +381,9 @@ __global__ __launch_bounds__(512, 1) void gemm_unit_k(float* __restrict__ sink, 
     v16f facc[4] = {zf, zf, zf, zf};
     v16f S = zf, R[2] = {zf, zf};
     v16i I[2] = {zi, zi};
+    const v32f z32 = {};
+    v32f S2 = z32;   // variant 0: scale products of a row-tile pair
+    const float saf = __uint_as_float(0x3F800000u ^ (t & 0x100)), sbf = __uint_as_float(0x3F000000u + t);
     for (int u = 0; u < units; u++) {
 #pragma unroll
         for (int ii = 0; ii < 4; ii++) {
@@ -392,18 +397,23 @@ __global__ __launch_bounds__(512, 1) void gemm_unit_k(float* __restrict__ sink, 
             v4h sau = sa;
             sau[0] ^= (short)(u * 4 + ii);
             if (VARIANT == 0) {
+                // the fold of row tile ii - 1 takes the high half of the pair buffer for
+                // odd tiles, the low half for even ones (tiles 3 and 0 of the previous
+                // unit / this one: high, then low after the (0, 1) products)
+                const int hi = (ii & 1) ^ 1;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     I[p] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b4, k ? I[p] : zi, 0, 0, 0);
 #pragma unroll
                     for (int r = 4 * k; r < 4 * k + 4; r++) {
-                        float v = fmaf((float)I[p ^ 1][r], S[r], facc[f][r]);
+                        float v = fmaf((float)I[p ^ 1][r], hi ? S2[16 + r] : S2[r], facc[f][r]);
                         asm volatile("" : "+v"(v));
                         facc[f][r] = v;
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                S = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sau, sb, zf, 0, 0, 0);
+                if (ii == 0 || ii == 2)
+                    S2 = __builtin_amdgcn_mfma_f32_32x32x1f32(saf + (float)(u * 4 + ii), sbf, z32, 0, 0, 0);
             } else {
                 R[p] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(sb, sau, zf, 0, 0, 0);   // the bias
 #pragma unroll
