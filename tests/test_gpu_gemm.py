@@ -255,7 +255,7 @@ def test_gemm_scale_products_over_wide_exponent_range(rt4, orc, torch_gpu):
 def test_gemm_full_precision_fp32_weight_scales(rt4, orc, torch_gpu):
     """wsc_gm holding arbitrary fp32 values (24 significant bits, not the fp16 values
     make_group_major produces) over a wide exponent range: the scale products are
-    formed from three bf16 parts of each scale, so every row matches the fp64 oracle
+    single fp32 products of the full scales, so every row matches the fp64 oracle
     to fp32 accuracy, for the int8 and the drop-in digit-plane entries alike."""
     M, N, K = 256, 320, 1024
     print(f"case gemm fp32 weight scales M={M} N={N} K={K}", flush=True)
