@@ -698,10 +698,14 @@ def main() -> int:
                 rt4_amd.gemv_w4a8_q(wq, ws, xq_gu, sa_gu, out=y_lm)
 
         lm_us = timed_graph(torch, gemv_lm) * 1e3 / len(lm)
-        kernels["gemv_lm_head_m4"] = {"us": round(lm_us, 3),
-                                      "GBs": round(gemv_kernel_bytes(M, 248320, 5120) / lm_us / 1e3, 1)}
+        lm_bytes = gemv_kernel_bytes(M, 248320, 5120)
+        kernels["gemv_lm_head_m4"] = {"us": round(lm_us, 3), "GBs": round(lm_bytes / lm_us / 1e3, 1)}
         del lm
         torch.cuda.empty_cache()
+        # its one-pass read ceiling: the same byte count through rt4p_hbm_read
+        pk = probe.hbm_read_ceiling(torch, lm_bytes, timed_graph)
+        kernels["gemv_lm_head_m4"].update({"measured_peak_us": pk["us"], "measured_peak_GBs": pk["GBs"],
+                                           "frac_measured": round(pk["us"] / lm_us, 4)})
 
     cpu = None
     if not args.no_cpu:

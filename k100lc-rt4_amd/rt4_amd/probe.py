@@ -86,6 +86,39 @@ def measure(torch, gib: float = 2.0) -> dict:
 READ_SHAPES = ((1024, 256), (1024, 512), (2048, 256), (2048, 512), (768, 512), (512, 512), (4096, 256))
 
 
+def hbm_read_ceiling(torch, nbytes: int, timed_graph, copies: int = 2, mults=(2, 4, 8)) -> dict:
+    """The fastest rt4p_hbm_read (grid-stride, 8 independent 16-byte loads per
+    lane in flight) of `nbytes` over `copies` distinct buffers replayed back to back
+    in a HIP graph, best over grids of cus * mult workgroups of 256 threads: the
+    one-pass read ceiling for sizes beyond rt4p_read_burst's reach (the LM head).
+    Returns {"us": per read, "GBs", "blocks"}."""
+    L = lib()
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    nb = nbytes // 16 * 16
+    bufs = [torch.empty(nb // 4, dtype=torch.int32, device="cuda").random_() for _ in range(copies)]
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    best = None
+    for mult in mults:
+        blocks = cus * mult
+
+        def fn():
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for b in bufs:
+                rc = L.rt4p_hbm_read(P(b), nb, P(sink), blocks, st)
+                if rc:
+                    raise RuntimeError(f"rt4p_hbm_read failed ({rc})")
+
+        fn()
+        torch.cuda.synchronize()
+        us = timed_graph(torch, fn) * 1e3 / copies
+        if best is None or us < best["us"]:
+            best = {"us": round(us, 3), "GBs": round(nb / us / 1e3, 1), "blocks": blocks}
+    del bufs
+    torch.cuda.empty_cache()
+    return best
+
+
 def read_ceiling(torch, nbytes: int, copies: int = 16, timed_graph=None) -> dict:
     """The fastest single launch reading `nbytes` from HBM: rt4p_read_burst over
     `copies` distinct buffers replayed back to back in a HIP graph (so no buffer
