@@ -668,6 +668,7 @@ def main() -> int:
             kernels["gemv_c0_m1"]["load_pattern"] = pattern_entry(pat_c0, c0_bytes, c0_us)
         kernels["ceilings"] = {"mfma_i32_16x16x64_i8_TOPS": probe.mfma_i8_rate(torch),
                                "mfma_i32_32x32x32_i8_TOPS": probe.mfma_i8_rate(torch, big=True),
+                               "mfma_f32_16x16x128_fp8_TOPS": probe.mfma_f8_16x16_rate(torch),
                                **probe.mfma_f8f6f4_rates(torch),
                                "gemm_unit_skeleton": probe.gemm_unit_cycles(torch),
                                "graph_node_us": probe.launch_cost(torch, timed_graph),
@@ -681,13 +682,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         kernels.update(gemm_table(torch, rt4_amd, workload, gen))
         kernels.update(attn_table(torch, rt4_amd, workload, gen))
-        # the same figures against the int8 MFMA issue rate measured on this box for the
-        # instruction each kernel runs (the GEMM 32x32x32, the attention 16x16x64)
+        # the same figures against the MFMA rate measured on this box for the instruction
+        # each kernel runs (the GEMM int8 32x32x32, the attention FP8 16x16x128)
         for key, rate in (("gemm_c2_gate_up", "mfma_i32_32x32x32_i8_TOPS"),
                           ("gemm_c2_down", "mfma_i32_32x32x32_i8_TOPS"),
                           ("gemm_ref_m2048", "mfma_i32_32x32x32_i8_TOPS"),
-                          ("attn_c4_prefill", "mfma_i32_16x16x64_i8_TOPS"),
-                          ("attn_ref_131k_prefill", "mfma_i32_16x16x64_i8_TOPS")):
+                          ("attn_c4_prefill", "mfma_f32_16x16x128_fp8_TOPS"),
+                          ("attn_ref_131k_prefill", "mfma_f32_16x16x128_fp8_TOPS")):
             tops = kernels[key].get("TOPS", kernels[key].get("TOPS_effective"))
             kernels[key]["frac_measured_issue"] = round(tops / kernels["ceilings"][rate], 4)
         lm = [workload.weights_torch(248320, 5120, generator=gen) for _ in range(2)]

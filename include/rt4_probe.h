@@ -51,6 +51,10 @@ int rt4p_empty(int blocks, int threads, void* stream);
  * each), 512 threads per block; fmt 0 FP8 E4M3, 2 FP6 E2M3, 4 FP4 E2M1 for both
  * operands. */
 int rt4p_mfma_f8f6f4(void* sink, int fmt, int iters, int blocks, void* stream);
+/* `iters` x 8 independent v_mfma_f32_16x16x128_f8f6f4 per wave (FP8 E4M3 operands,
+ * no block scale, 32768 MACs each), 512 threads per block: the instruction the
+ * attention kernel issues. */
+int rt4p_mfma_f8_16x16(void* sink, int iters, int blocks, void* stream);
 /* `units` iterations of the prefill GEMM's per-unit instruction skeleton (registers
  * only) per wave, 512 threads per block: variant 0 the int8 form, 1 the FP8-digit
  * form (see probe.hip). */

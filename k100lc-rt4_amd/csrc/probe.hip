@@ -26,6 +26,8 @@
 //   rt4p_empty      an empty kernel: the per-launch cost of a graph node
 //   rt4p_mfma_f8f6f4 back-to-back v_mfma_scale_f32_32x32x64_f8f6f4 with FP8, FP6 or
 //                   FP4 operands (the matrix-core rate per format)
+//   rt4p_mfma_f8_16x16 back-to-back v_mfma_f32_16x16x128_f8f6f4 (FP8, no block
+//                   scale), the form the attention kernel issues, 8 chains per wave
 //   rt4p_gemm_unit  the prefill GEMM's per-unit instruction skeleton without memory:
 //                   per wave and 128-wide K group, four 32x32 row tiles of MFMAs with
 //                   the previous row tile's fold interleaved, at the GEMM's occupancy
@@ -44,6 +46,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
@@ -340,6 +343,30 @@ hipError_t launch_gemv_loads(const uint32_t* wq, const uint16_t* ws, const int8_
 __global__ void empty_k() {}
 
 // ---- scaled f8f6f4 MFMA rate: four independent accumulator chains per wave.
+// 8 independent chains of the unscaled 16x16x128 FP8 MFMA per wave (the scale
+// builtin with zero scales compiles to the unscaled instruction).
+__global__ __launch_bounds__(512) void mfma_f8_16_k(float* __restrict__ sink, int iters, int seed) {
+    v8i a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (seed * (i + 1) + (int)threadIdx.x) & 0x3f3f3f3f;
+        b[i] = (seed ^ (i * 77 + (int)threadIdx.x)) & 0x0f0f0f0f;
+    }
+    v4f c[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) c[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4((j & 1) ? a : b, (j & 2) ? a : b, c[j], 0, 0,
+                                                                    0, 0, 0, 0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (s == 1234.5f) sink[blockIdx.x] = s;
+}
+
 template <int FMT>
 __global__ __launch_bounds__(512) void mfma_f8f6f4_k(float* __restrict__ sink, int iters, int seed) {
     v8i a, b;
@@ -552,6 +579,13 @@ int rt4p_gemv_loads(const void* wq, const void* ws, const void* xq, const void* 
 int rt4p_empty(int blocks, int threads, void* stream) {
     if (blocks < 1 || threads < 1 || threads > 1024) return 1;
     hipLaunchKernelGGL(empty_k, dim3(blocks), dim3(threads), 0, (hipStream_t)stream);
+    return last() == hipSuccess ? 0 : 3;
+}
+
+int rt4p_mfma_f8_16x16(void* sink, int iters, int blocks, void* stream) {
+    if (!sink || iters < 1 || blocks < 1) return 1;
+    hipLaunchKernelGGL(mfma_f8_16_k, dim3(blocks), dim3(512), 0, (hipStream_t)stream, static_cast<float*>(sink),
+                       iters, 12345);
     return last() == hipSuccess ? 0 : 3;
 }
 

@@ -7,7 +7,7 @@ import pathlib
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "librt4probe.so"
 EXPORTS = ("rt4p_hbm_read", "rt4p_read_burst", "rt4p_copy", "rt4p_mfma_i8", "rt4p_valu_fma", "rt4p_gemv_loads",
-           "rt4p_empty", "rt4p_mfma_f8f6f4", "rt4p_gemm_unit")
+           "rt4p_empty", "rt4p_mfma_f8f6f4", "rt4p_mfma_f8_16x16", "rt4p_gemm_unit")
 _lib = None
 
 
@@ -24,7 +24,8 @@ def lib() -> ctypes.CDLL:
                 "rt4p_copy": [P, P, Z, I, P],
                 "rt4p_mfma_i8": [P, I, I, I, P], "rt4p_valu_fma": [P, I, I, P],
                 "rt4p_gemv_loads": [P, P, P, P, P, I, I, I, I, I, I, I, P], "rt4p_empty": [I, I, P],
-                "rt4p_mfma_f8f6f4": [P, I, I, I, P], "rt4p_gemm_unit": [P, I, I, I, P]}
+                "rt4p_mfma_f8f6f4": [P, I, I, I, P], "rt4p_mfma_f8_16x16": [P, I, I, P],
+                "rt4p_gemm_unit": [P, I, I, I, P]}
         for name, args in sigs.items():
             getattr(L, name).argtypes = args
             getattr(L, name).restype = ctypes.c_int
@@ -153,7 +154,8 @@ def read_ceiling(torch, nbytes: int, copies: int = 16, timed_graph=None) -> dict
 
 def mfma_i8_rate(torch, big: bool = False, iters: int = 2048) -> float:
     """Measured dense int8 MFMA rate in TOPS (v_mfma_i32_16x16x64_i8, or 32x32x32
-    when big): 8 waves per SIMD, 4 independent accumulator chains per wave."""
+    when big): 8 waves per SIMD, 4 independent accumulator chains per wave (8 chains
+    of the 16x16 form measured lower, 2.6-2.9 against 3.5 POP/s)."""
     L = lib()
     cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
     sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
@@ -217,6 +219,18 @@ def launch_cost(torch, timed_graph, n: int = 64) -> float:
     fn()
     torch.cuda.synchronize()
     return round(timed_graph(torch, fn) * 1e3 / n, 3)
+
+
+def mfma_f8_16x16_rate(torch, iters: int = 2048) -> float:
+    """Measured dense rate (TOPS) of v_mfma_f32_16x16x128_f8f6f4 with FP8 operands and
+    no block scale, as the attention kernel issues it: 2 waves per SIMD, 8
+    independent accumulator chains per wave."""
+    L = lib()
+    cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ms = _timed(torch, lambda: L.rt4p_mfma_f8_16x16(ctypes.c_void_p(sink.data_ptr()), iters, cus, st))
+    return round(2.0 * 32768 * 8 * iters * 8 * cus / ms / 1e9, 1)
 
 
 def mfma_f8f6f4_rates(torch, iters: int = 2048) -> dict:

@@ -46,6 +46,8 @@ def test_probe_argument_checks_return_before_any_launch():
     assert L.rt4p_copy(fake, None, 4096, 4, None) == 1
     assert L.rt4p_mfma_i8(fake, 1, 0, 4, None) == 1
     assert L.rt4p_valu_fma(fake, 0, 4, None) == 1
+    assert L.rt4p_mfma_f8_16x16(None, 4, 4, None) == 1
+    assert L.rt4p_mfma_f8_16x16(fake, 0, 4, None) == 1
 
 
 def _write_csv(path, rows):
