@@ -105,3 +105,21 @@ def test_gemm_on_rowwise_activations(rt4, orc, torch_gpu):
     err = rel_l2(host(out).ravel(), ref.ravel())
     print(f"  rel_l2 = {err:.3e}")
     assert err < TIGHT
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_rowwise_unaligned_input_matches_aligned(rt4, torch_gpu, mode):
+    """x 4 bytes off 16-byte alignment takes the element-load path: same bits."""
+    M, K = 3, 5120
+    print(f"case rowwise unaligned mode={mode}", flush=True)
+    x = _acts(83, M, K, zero_row=True)
+    xa = dev(torch_gpu, x)
+    buf = torch_gpu.empty(M * K + 1, dtype=torch_gpu.float32, device="cuda")
+    xu = buf[1:].view(M, K)
+    xu.copy_(xa)
+    assert xu.data_ptr() % 16 != 0
+    ra = rt4.quant_act_rowwise(xa, mode=mode)
+    ru = rt4.quant_act_rowwise(xu, mode=mode)
+    torch_gpu.cuda.synchronize()
+    for a, b in zip(ra, ru):
+        assert np.array_equal(host(a), host(b))
