@@ -609,6 +609,31 @@ def test_attention_benchmark_shape_against_reference_kernel(rt4, orc, torch_gpu,
         e_ref, e_our = rel_l2(ref_o[h, rows], alg), rel_l2(our_o[h, rows], alg)
         print(f"  head {h}: vs the fp64 algorithm model: reference kernel {e_ref:.2e}, ours {e_our:.2e}")
         worst = max(worst, e_ref, e_our)
+    # Every row where the two kernels differ by more than 1e-4, against the fp64 model:
+    # such a row holds a 3-bit P code that a kernel's fp32 scores put on the other side
+    # of a rounding edge from the model.  Both kernels do this on a few rows (seed 31:
+    # 118 rows of 24576 differ; ours is off the model on 58, the reference kernel on 62,
+    # both on 2), so ours must flip no more rows than the reference kernel, give or take
+    # a few, and by no larger an error.
+    d = np.linalg.norm(our_o - ref_o, axis=2) / np.maximum(np.linalg.norm(ref_o, axis=2), 1e-30)   # [H, n_q]
+    rows_off = np.argwhere(d > 1e-4)
+    print(f"  rows where the kernels differ by more than 1e-4: {len(rows_off)} of {H * n_q}")
+    assert len(rows_off) <= 256
+    ours_off = ref_off = both_off = 0
+    worst_row_ours = worst_row_ref = 0.0
+    for h in np.unique(rows_off[:, 0]):
+        rr = rows_off[rows_off[:, 0] == h, 1].astype(np.int32)
+        alg = orc.fa_rows(*c, n_q, n_kv, ctx, n_kv, ratio, int(h), rr, 1).reshape(len(rr), HD)
+        for i, r in enumerate(rr):
+            e_ref, e_our = rel_l2(ref_o[h, r], alg[i]), rel_l2(our_o[h, r], alg[i])
+            ours_off += e_our > 1e-4
+            ref_off += e_ref > 1e-4
+            both_off += (e_our > 1e-4) and (e_ref > 1e-4)
+            worst_row_ours, worst_row_ref = max(worst_row_ours, e_our), max(worst_row_ref, e_ref)
+    print(f"  of those, off the fp64 model by more than 1e-4: ours {ours_off}, the reference kernel "
+          f"{ref_off}, both {both_off}; worst row: ours {worst_row_ours:.2e}, reference {worst_row_ref:.2e}")
+    assert ours_off <= ref_off + 8
+    assert worst_row_ours <= max(worst_row_ref, 2e-2)
     # each fp32 kernel is within 1e-4 of the fp64 model (a score that lands on a
     # rounding edge of a 3-bit P code may round either way in fp32); the two
     # kernels' outputs may then differ by up to the sum of their deviations
