@@ -738,6 +738,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         // -- and re-arms the counter for the next call.  No workgroup waits for
         // another.
         constexpr int kSc1 = 16;    // cache policy: sc1
+        constexpr int kFastSplits = 4;   // split counts combined with loads issued in bulk
         const int item = head * gridDim.x + blockIdx.x;
         // this query block's 64 rows of split s: O [64][HD] and (m, L) [64]
         auto o_rsrc = [&](int s) {
@@ -772,23 +773,64 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                 const v2u v = __builtin_amdgcn_raw_buffer_load_b64(ml_rsrc(s), moff, 0, kSc1);
                 return make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
             };
-            float Mx = -__builtin_inff();
-            for (int s = 0; s < nsplit; s++) Mx = fmaxf(Mx, ml_of(s).x);
             float o[16][4];
 #pragma unroll
             for (int dt = 0; dt < 16; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) o[dt][r] = 0.f;
             float l = 0.f;
-            for (int s = 0; s < nsplit; s++) {
-                const float2 ml = ml_of(s);
-                const float a = exp2f(ml.x - Mx);
-                if (s == split) {      // this workgroup's own split, still in registers
+            if (nsplit <= kFastSplits) {
+                // All loads of a round are issued before any is used: every split's
+                // (m, L) in one round, then the partial O in four rounds of 64 dims,
+                // each holding that quarter of every split (5 memory round trips in
+                // place of 2·nsplit + 1 dependent ones).  This workgroup's own split
+                // is read back like the others (its stores completed at vmcnt(0)
+                // above).  The sums run in split order, as in the general path.
+                float2 ml[kFastSplits];
 #pragma unroll
-                    for (int dt = 0; dt < 16; dt++)
+                for (int s = 0; s < kFastSplits; s++)
+                    if (s < nsplit) ml[s] = ml_of(s);
+                float Mx = -__builtin_inff();
 #pragma unroll
-                        for (int r = 0; r < 4; r++) o[dt][r] = fmaf(a, O[dt][r], o[dt][r]);
-                } else {
+                for (int s = 0; s < kFastSplits; s++)
+                    if (s < nsplit) Mx = fmaxf(Mx, ml[s].x);
+                float a[kFastSplits];
+#pragma unroll
+                for (int s = 0; s < kFastSplits; s++)
+                    if (s < nsplit) {
+                        a[s] = exp2f(ml[s].x - Mx);
+                        l = fmaf(a[s], ml[s].y, l);
+                    }
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    v4u b[kFastSplits][4];
+#pragma unroll
+                    for (int s = 0; s < kFastSplits; s++)
+                        if (s < nsplit) {
+                            const __amdgpu_buffer_rsrc_t rs = o_rsrc(s);
+#pragma unroll
+                            for (int d = 0; d < 4; d++)
+                                b[s][d] = __builtin_amdgcn_raw_buffer_load_b128(rs, ooff + (4 * c + d) * 64, 0, kSc1);
+                        }
+#pragma unroll
+                    for (int s = 0; s < kFastSplits; s++)
+                        if (s < nsplit) {
+#pragma unroll
+                            for (int d = 0; d < 4; d++) {
+                                const int dt = 4 * c + d;
+                                o[dt][0] = fmaf(a[s], __uint_as_float(b[s][d].x), o[dt][0]);
+                                o[dt][1] = fmaf(a[s], __uint_as_float(b[s][d].y), o[dt][1]);
+                                o[dt][2] = fmaf(a[s], __uint_as_float(b[s][d].z), o[dt][2]);
+                                o[dt][3] = fmaf(a[s], __uint_as_float(b[s][d].w), o[dt][3]);
+                            }
+                        }
+                }
+            } else {
+                float Mx = -__builtin_inff();
+                for (int s = 0; s < nsplit; s++) Mx = fmaxf(Mx, ml_of(s).x);
+                for (int s = 0; s < nsplit; s++) {
+                    const float2 ml = ml_of(s);
+                    const float a = exp2f(ml.x - Mx);
                     const __amdgpu_buffer_rsrc_t rs = o_rsrc(s);
 #pragma unroll
                     for (int dt = 0; dt < 16; dt++) {
@@ -798,8 +840,8 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                         o[dt][2] = fmaf(a, __uint_as_float(v.z), o[dt][2]);
                         o[dt][3] = fmaf(a, __uint_as_float(v.w), o[dt][3]);
                     }
+                    l = fmaf(a, ml.y, l);
                 }
-                l = fmaf(a, ml.y, l);
             }
             float* orow = out + (size_t)qrow * HD + 4 * G;
 #pragma unroll
