@@ -9,8 +9,9 @@
  *
  * Library scratch: the drop-in linears' quantized activations, the split
  * workspaces of the GEMVs (W4A8 and W4A4 share one, partials plus counters that
- * every launch leaves at zero), of the GEMM and of the attention prefill are one
- * buffer per device and kind, grown on demand like the reference's static
+ * every launch leaves at zero), of the GEMM and of the attention prefill, and the
+ * prefill's staged K/V copy (32 KB per key tile and KV head) are one buffer per
+ * device and kind, grown on demand like the reference's static
  * scratch (src/k_gemv.hip:16-23).  Calls that may run at the same time on one
  * device (different streams) therefore race on it; the caller orders them, as
  * it must for the reference.  An outgrown buffer is kept allocated until
@@ -20,7 +21,8 @@
  * Nothing is allocated while `stream` is being captured: a call that would
  * have to grow a scratch buffer then fails with RT4_E_CAPTURE, except that the
  * split GEMV and the attention prefill (automatic split count) fall back to
- * their unsplit forms, which need no workspace.
+ * their unsplit forms, which need no workspace, and the prefill without room for
+ * its staged K/V copy stages the tiles in every workgroup (same results).
  *
  * Formats (docs/FORMAT.md:61-73 of the reference, unchanged here):
  *   wq   uint32 [N][K/8]   RT4 int4 weights: dword d holds k = 8d..8d+7, nibble e
@@ -254,7 +256,10 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
  * algorithm: per 64-key tile P = clamp(int(7 exp(s - m_tile) + 0.5), 0, 7) and
  * online rescaling (the running reference moves only when a tile's max exceeds
  * it by more than a factor 2^8: the same O and L, rounded differently).  Query
- * row i has position off + i.  Replaces the prefill
+ * row i has position off + i.  K/V are staged once per call (codes unpacked into
+ * the MFMA operand bytes, 32 KB per key tile and KV head of library scratch; at
+ * most 4 GiB, beyond which each workgroup stages its own tiles), then DMA'd into
+ * LDS by the workgroups.  Replaces the prefill
  * branch of k_attention (src/kernels.h:81, src/k_fa.hip:282-300; kernel fa_int4,
  * kernels/flash_attn_core.h:74-435).  n_q % 64 == 0, kv_cap % 64 == 0,
  * n_tile * 64 <= kv_cap, kv_cap <= 16777152 (2^24 - 64: one KV head's cache is

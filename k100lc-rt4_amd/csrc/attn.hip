@@ -49,9 +49,15 @@
 //                         that key order a V operand dword is exactly the even-
 //                         or odd-key bytes of one V cache dword.
 // Row max over a query's 64 keys is 15 in-lane ops plus two cross-lane steps
-// (xor 16, xor 32).  The workgroup unpacks each K/V tile once into LDS in MFMA
-// operand order (16 bytes per (subtile, group, half, lane)), so the waves only
-// issue ds_read_b128 of ready operands.  Tiles past the workgroup's last query
+// (xor 16, xor 32).  The K/V tiles reach LDS in MFMA operand order (16 bytes per
+// (subtile, group, half, lane)), so the waves only issue ds_read_b128 of ready
+// operands.  A pre-pass (fa_expand_kv_k) unpacks every tile once per call into a
+// copy in memory with exactly that layout, and the workgroups move each tile into
+// LDS with global_load_lds_dwordx4 (no registers, no unpacking, no LDS stores):
+// unpacking in every workgroup repeated it once per query block and split, about a
+// tenth of the kernel at C4.  Without room for the copy (graph capture before the
+// first eager call, or a copy beyond 4 GiB) each workgroup stages its tiles itself
+// from the packed cache, with the same bytes.  Tiles past the workgroup's last query
 // position are skipped: the reference processes them but every entry is masked,
 // which leaves its state bit-for-bit unchanged.  The tile loop is a two-tile
 // pipeline (S and P of the next tile beside the PV product of the current one;
@@ -142,6 +148,48 @@ __device__ __forceinline__ uint32_t codes8(const float* v, float s) {
         for (int e = 0; e < 8; e++) w |= code4(v[e], s) << (4 * e);
     }
     return w;
+}
+
+constexpr int kRsrcW3 = 0x00020000;    // dword 3 of a buffer resource: 32-bit data format
+
+// The staged form of a 64-key tile: the MFMA operand bytes in the order the waves
+// read them, 16 KB for K and 16 KB for V.  These write one thread's share of a
+// tile's block (in LDS, or its copy in memory for the DMA path).
+//
+// K: key kk = tid % 64, dims 64p .. 64p + 63 (p = tid / 64, code dwords j = 0..7,
+// k0 then k1): group p/2, lane group G' = 2(p%2) + j/4 of the operand, half (j/2)%2
+// of its 32 bytes.  Piece (subtile, group, half) is 64 lanes x 16 bytes; the key's
+// lane in it is 16G' + slot of kk%16.  Every nibble c becomes the byte c + 8.
+__device__ __forceinline__ void put_k_slots(unsigned char* blk, v4u k0, v4u k1, int tid) {
+    const int kk = tid & 63, p = tid >> 6;
+    const uint32_t d[8] = {k0.x ^ 0x88888888u, k0.y ^ 0x88888888u, k0.z ^ 0x88888888u, k0.w ^ 0x88888888u,
+                           k1.x ^ 0x88888888u, k1.y ^ 0x88888888u, k1.z ^ 0x88888888u, k1.w ^ 0x88888888u};
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const uint4 v = make_uint4(even_e4m3(d[2 * g]), odd_e4m3(d[2 * g]), even_e4m3(d[2 * g + 1]),
+                                   odd_e4m3(d[2 * g + 1]));
+        const int piece = ((kk >> 4) * 2 + (p >> 1)) * 2 + (g & 1);
+        *reinterpret_cast<uint4*>(blk + (piece * 64 + 16 * (2 * (p & 1) + (g >> 1)) + slot_of_key(kk & 15)) * 16) = v;
+    }
+}
+// V: dim tid, the code dwords of its eight 8-key groups.  Lane G*16 + d%16 of dim
+// tile d/16 gets, in dword t = 0..3, the offset-code bytes of the even (G even) or
+// odd keys of 8-key group 2t + G/2 -- keys 16t + key_of_slot(G, r), r = 0..3, as P
+// holds them.
+__device__ __forceinline__ void put_v_slots(unsigned char* blk, const uint32_t (&vw)[8], int tid) {
+    uint32_t e[8], o[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t w8 = vw[g] ^ 0x88888888u;
+        e[g] = even_e4m3(w8);
+        o[g] = odd_e4m3(w8);
+    }
+#pragma unroll
+    for (int G = 0; G < 4; G++) {
+        const uint32_t* src = (G & 1) ? o : e;
+        const uint4 v = make_uint4(src[G >> 1], src[2 + (G >> 1)], src[4 + (G >> 1)], src[6 + (G >> 1)]);
+        *reinterpret_cast<uint4*>(blk + ((tid >> 4) * 64 + G * 16 + (tid & 15)) * 16) = v;
+    }
 }
 
 }  // namespace
@@ -333,6 +381,7 @@ __global__ __launch_bounds__(256) void kv_stage_v64_k(float* __restrict__ stage,
 
 // ---------------------------------------------------------------- prefill --
 
+template <bool DMA>
 __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__ qq,
                                                     const float* __restrict__ qsc,
                                                     const uint32_t* __restrict__ kc,
@@ -341,7 +390,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
                                                     const float* __restrict__ vsc, float* __restrict__ out,
                                                     int n_q, int n_kv, int off, int n_tile, int ratio,
                                                     int kv_cap, int nsplit, float* __restrict__ opart,
-                                                    float2* __restrict__ mlpart, int* __restrict__ cnt) {
+                                                    float2* __restrict__ mlpart, int* __restrict__ cnt,
+                                                    const unsigned char* __restrict__ kx,
+                                                    const unsigned char* __restrict__ vx) {
     __shared__ __align__(16) unsigned char ku[2 * KU_BYTES];   // x2: [subtile][k-step][lane] x 16 B
     __shared__ __align__(16) unsigned char vu[2 * VU_BYTES];   // x2: [dim tile][lane] x 16 B
     __shared__ __align__(16) float ks_l[2][2 * BNK];
@@ -438,7 +489,6 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // kv_cap are replaced by 1 when the stage is unpacked.  No load is conditional
     // or clamped: selecting right after a load, or loading under a condition,
     // makes the compiler wait for the load there, which would defeat the prefetch.
-    constexpr int kRsrcW3 = 0x00020000;    // dword 3 of the resource: 32-bit data format
     const __amdgpu_buffer_rsrc_t rs_k =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(kc), 0, n_kv * KDW * 4, kRsrcW3);
     const __amdgpu_buffer_rsrc_t rs_v =
@@ -456,58 +506,55 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     // zeros (checked on the CPU by tests/test_attention.py).
     auto load_k = [&](StageK& S, int t) {
         const int sk = (int)((uint32_t)t * (uint32_t)(BNK * KDW * 4));
-        S.k0 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k, sk, 0);
-        S.k1 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k + 16, sk, 0);
+        if constexpr (!DMA) {
+            S.k0 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k, sk, 0);
+            S.k1 = __builtin_amdgcn_raw_buffer_load_b128(rs_k, off_k + 16, sk, 0);
+        }
         S.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_ks, off_ks, t * BNK * 4, 0));
     };
     auto load_v = [&](StageV& S, int t) {
         const int sv = (int)((uint32_t)t * (uint32_t)(BNK / 8 * HD * 4));
+        if constexpr (!DMA) {
 #pragma unroll
-        for (int g = 0; g < 8; g++)
-            S.v[g] = __builtin_amdgcn_raw_buffer_load_b32(rs_v, tid * 4 + (g & 3) * HD * 4,
-                                                          sv + (g >> 2) * 4 * HD * 4, 0);
+            for (int g = 0; g < 8; g++)
+                S.v[g] = __builtin_amdgcn_raw_buffer_load_b32(rs_v, tid * 4 + (g & 3) * HD * 4,
+                                                              sv + (g >> 2) * 4 * HD * 4, 0);
+        }
         S.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_vs, tid * 4, t * HD * 4, 0));
     };
     auto store_k = [&](const StageK& S, int b, int t) {
-        // Key kk, dims 64p .. 64p + 63 (code dwords j = 0..7): group p/2, lane group
-        // G' = 2(p%2) + j/4 of the operand, half (j/2)%2 of its 32 bytes.  Piece
-        // (subtile, group, half) is 64 lanes x 16 bytes; the key's lane in it is
-        // 16G' + slot of kk%16.  Keys >= n_kv read as zero codes
-        // (flash_attn_core.h:143-147), i.e. bytes 8.
-        unsigned char* kub = ku + b * KU_BYTES;
-        const int kk = tid & 63, p = tid >> 6;
-        const uint32_t d[8] = {S.k0.x ^ 0x88888888u, S.k0.y ^ 0x88888888u, S.k0.z ^ 0x88888888u,
-                               S.k0.w ^ 0x88888888u, S.k1.x ^ 0x88888888u, S.k1.y ^ 0x88888888u,
-                               S.k1.z ^ 0x88888888u, S.k1.w ^ 0x88888888u};
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint4 v = make_uint4(even_e4m3(d[2 * g]), odd_e4m3(d[2 * g]), even_e4m3(d[2 * g + 1]),
-                                       odd_e4m3(d[2 * g + 1]));
-            const int piece = ((kk >> 4) * 2 + (p >> 1)) * 2 + (g & 1);
-            *reinterpret_cast<uint4*>(kub + (piece * 64 + 16 * (2 * (p & 1) + (g >> 1)) + slot_of_key(kk & 15)) * 16) = v;
-        }
+        // codes (unless DMA brings them) and scales; keys >= n_kv read as zero codes
+        // (flash_attn_core.h:143-147), i.e. bytes 8
+        if constexpr (!DMA) put_k_slots(ku + b * KU_BYTES, S.k0, S.k1, tid);
         if (tid < 2 * BNK) ks_l[b][tid] = t * BNK + (tid & 63) < kv_cap ? S.ks : 1.f;
     };
     auto store_v = [&](const StageV& S, int b, int t) {
-        // lane G*16 + d%16 of dim tile d/16 gets, in dword t = 0..3, the offset-code
-        // bytes of the even (G even) or odd keys of 8-key group 2t + G/2 -- keys
-        // 16t + key_of_slot(G, r), r = 0..3, as P holds them; a group of 8 keys is
-        // read only if it is whole (flash_attn_core.h:150-152), else zero codes
-        unsigned char* vub = vu + b * VU_BYTES;
-        uint32_t e[8], o[8];
-#pragma unroll
-        for (int g = 0; g < 8; g++) {
-            const uint32_t w8 = S.v[g] ^ 0x88888888u;
-            e[g] = even_e4m3(w8);
-            o[g] = odd_e4m3(w8);
-        }
-#pragma unroll
-        for (int G = 0; G < 4; G++) {
-            const uint32_t* src = (G & 1) ? o : e;
-            const uint4 v = make_uint4(src[G >> 1], src[2 + (G >> 1)], src[4 + (G >> 1)], src[6 + (G >> 1)]);
-            *reinterpret_cast<uint4*>(vub + ((tid >> 4) * 64 + G * 16 + (tid & 15)) * 16) = v;
-        }
+        // a group of 8 keys is read only if it is whole (flash_attn_core.h:150-152),
+        // else zero codes
+        if constexpr (!DMA) put_v_slots(vu + b * VU_BYTES, S.v, tid);
         vs_l[b][tid] = t < kv_cap / BNK ? S.vs : 1.f;
+    };
+    // DMA path: tiles t of K and V as staged blocks from the expanded copy (kx, vx:
+    // [KV head][tile][16 KB]) straight into LDS buffers bk / bv, one 1 KB piece per
+    // instruction, four per wave.  Tiles past the last one (the prefetch runs ahead)
+    // read the last tile instead, into buffers nobody reads.
+    auto dma_k = [&](int t, int b) {
+        t = t < n_tile - 1 ? t : n_tile - 1;
+        const unsigned char* src = kx + ((size_t)vh * n_tile + t) * KU_BYTES;
+        const uint32_t dst = lds_addr(ku) + b * KU_BYTES + 4 * w * 1024;
+        dma16<0>(lane * 16 + 4 * w * 1024, src, dst);
+        dma16<1024>(lane * 16 + (4 * w + 1) * 1024, src, dst);
+        dma16<2048>(lane * 16 + (4 * w + 2) * 1024, src, dst);
+        dma16<3072>(lane * 16 + (4 * w + 3) * 1024, src, dst);
+    };
+    auto dma_v = [&](int t, int b) {
+        t = t < n_tile - 1 ? t : n_tile - 1;
+        const unsigned char* src = vx + ((size_t)vh * n_tile + t) * VU_BYTES;
+        const uint32_t dst = lds_addr(vu) + b * VU_BYTES + 4 * w * 1024;
+        dma16<0>(lane * 16 + 4 * w * 1024, src, dst);
+        dma16<1024>(lane * 16 + (4 * w + 1) * 1024, src, dst);
+        dma16<2048>(lane * 16 + (4 * w + 2) * 1024, src, dst);
+        dma16<3072>(lane * 16 + (4 * w + 3) * 1024, src, dst);
     };
 
     const v4f cS0 = {cS[0], cS[0], cS[0], cS[0]}, cS1 = {cS[1], cS[1], cS[1], cS[1]};
@@ -684,6 +731,11 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         const int t_mask = (off + q0 + 1) / BNK;
         StageK sk;
         StageV sv;
+        if constexpr (DMA) {
+            dma_k(t0, t0 & 1);
+            dma_v(t0, t0 & 1);
+            dma_k(t0 + 1, (t0 + 1) & 1);
+        }
         load_k(sk, t0);
         load_v(sv, t0);
         store_k(sk, t0 & 1, t0);
@@ -692,6 +744,7 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
         store_k(sk, (t0 + 1) & 1, t0 + 1);
         load_k(sk, t0 + 2);
         load_v(sv, t0 + 1);
+        if constexpr (DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         Front f = t0 >= t_mask ? front(t0, t0 & 1, std::true_type{}) : front(t0, t0 & 1, std::false_type{});
         __syncthreads();     // K buffer t0&1 is rewritten in the first iteration
@@ -699,6 +752,14 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             const float pbv = update(fc);
             store_k(sk, t & 1, t + 2);
             store_v(sv, (t + 1) & 1, t + 1);
+            // K(t + 2) into the buffer K(t) left, V(t + 1) into the one V(t - 1) left.
+            // Issued after the scale stores above: the compiler does not count these
+            // loads, and its wait for the scale loads it issued last iteration would
+            // otherwise wait for them too.
+            if constexpr (DMA) {
+                dma_k(t + 2, t & 1);
+                dma_v(t + 1, (t + 1) & 1);
+            }
             load_k(sk, t + 3);
             load_v(sv, t + 2);
             // keep the loads here: left to itself the compiler sinks them next to
@@ -706,6 +767,9 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
             asm volatile("" ::: "memory");
             const Front fn = front(t + 1, (t + 1) & 1, mask_tag);
             back(fc.p_lo, fc.p_hi, fc.corr, pbv, t & 1);
+            // the tiles DMA'd above have landed in LDS before the barrier (the two scale
+            // loads issued after them may still be in flight)
+            if constexpr (DMA) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
             __syncthreads();
             return fn;
         };
@@ -854,6 +918,37 @@ __global__ __launch_bounds__(NTA, 2) void fa_int4_k(const uint32_t* __restrict__
     }
 }
 
+// Staged K/V blocks of every tile of every KV head, for the DMA path: the kernel's
+// own staging (same loads, range checks and byte layout), run once per call instead
+// of once per query block and split.  Block (vh, t) of kx / vx holds the 16 KB that
+// tile t's staging writes to LDS.
+__global__ __launch_bounds__(256) void fa_expand_kv_k(const uint32_t* __restrict__ kc,
+                                                      const uint32_t* __restrict__ vc,
+                                                      unsigned char* __restrict__ kx,
+                                                      unsigned char* __restrict__ vx, int n_kv, int n_tile,
+                                                      int kv_cap) {
+    const int t = blockIdx.x, vh = blockIdx.y, tid = threadIdx.x;
+    const size_t blk = ((size_t)vh * n_tile + t) * KU_BYTES;
+    if (blockIdx.z == 0) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(kc + (size_t)vh * kv_cap * KDW), 0, n_kv * KDW * 4, kRsrcW3);
+        const int off = ((tid & 63) * KDW + 8 * (tid >> 6)) * 4;
+        const int sk = (int)((uint32_t)t * (uint32_t)(BNK * KDW * 4));
+        const v4u k0 = __builtin_amdgcn_raw_buffer_load_b128(rs, off, sk, 0);
+        const v4u k1 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, sk, 0);
+        put_k_slots(kx + blk, k0, k1, tid);
+    } else {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(vc + (size_t)vh * (kv_cap / 8) * HD), 0, (n_kv / 8) * HD * 4, kRsrcW3);
+        const int sv = (int)((uint32_t)t * (uint32_t)(BNK / 8 * HD * 4));
+        uint32_t vw[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++)
+            vw[g] = __builtin_amdgcn_raw_buffer_load_b32(rs, tid * 4 + (g & 3) * HD * 4, sv + (g >> 2) * 4 * HD * 4, 0);
+        put_v_slots(vx + blk, vw, tid);
+    }
+}
+
 // -------------------------------------------------------------- launchers --
 
 hipError_t launch_attn_q_quant(uint32_t* qq, float* qs, const float* x, int T, int H, int D, int G, int TP,
@@ -937,13 +1032,30 @@ size_t fa_cnt_bytes(int n_q, int n_heads, int nsplit) {
     return nsplit > 1 ? (size_t)(n_q / QROWS) * n_heads * sizeof(int) : 0;
 }
 
+size_t fa_kvx_bytes(int n_heads, int ratio, int n_tile) {
+    return (size_t)2 * (size_t)(n_heads / ratio) * (size_t)n_tile * KU_BYTES;
+}
+
 hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                           const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
-                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, hipStream_t st) {
+                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, void* kvx,
+                          hipStream_t st) {
     float* opart = part;
     float2* mlpart = part ? reinterpret_cast<float2*>(part + (size_t)nsplit * n_heads * n_q * HD) : nullptr;
-    hipLaunchKernelGGL(fa_int4_k, dim3(n_q / QROWS, n_heads, nsplit), dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc,
-                       out, n_q, n_kv, off, n_tile, ratio, kv_cap, nsplit, opart, mlpart, cnt);
+    const dim3 grid(n_q / QROWS, n_heads, nsplit);
+    if (!kvx) {
+        hipLaunchKernelGGL(fa_int4_k<false>, grid, dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc, out, n_q, n_kv, off,
+                           n_tile, ratio, kv_cap, nsplit, opart, mlpart, cnt, nullptr, nullptr);
+        return hipGetLastError();
+    }
+    const int kvh = n_heads / ratio;
+    unsigned char* kx = static_cast<unsigned char*>(kvx);
+    unsigned char* vx = kx + (size_t)kvh * n_tile * KU_BYTES;
+    hipLaunchKernelGGL(fa_expand_kv_k, dim3(n_tile, kvh, 2), dim3(256), 0, st, kc, vc, kx, vx, n_kv, n_tile, kv_cap);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(fa_int4_k<true>, grid, dim3(NTA), 0, st, qq, qsc, kc, ksc, vc, vsc, out, n_q, n_kv, off,
+                       n_tile, ratio, kv_cap, nsplit, opart, mlpart, cnt, kx, vx);
     return hipGetLastError();
 }
 

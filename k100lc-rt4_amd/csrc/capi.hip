@@ -35,7 +35,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // the retired buffers of a slot add up to at most twice its final size.  Not
 // safe for concurrent calls from several threads (the reference's scratch has
 // the same property, src/k_gemv.hip:47-51).
-enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlotAttnCnt = 8, kSlots = 9 };
+enum Slot { kSlotActQ = 0, kSlotActS = 1, kSlotGemmA = 2, kSlotGemmPart = 3, kSlotGemmCnt = 4, kSlotAttnPart = 5, kSlotGemvPart = 6, kSlotGemvCnt = 7, kSlotAttnCnt = 8, kSlotAttnKV = 9, kSlots = 10 };
 constexpr int kMaxDev = 64;
 struct Buf {
     void* p = nullptr;
@@ -695,6 +695,8 @@ int rt4_kv_append_v(uint32_t* vc, float* vsc, float* stage, const float* vf, int
 // The prefill kernel addresses one KV head's cache through 32-bit buffer offsets
 // (kv_cap * 128 bytes of K codes, plus up to three tiles read past the end).
 constexpr int kMaxKvCap = (1 << 24) - 64;
+// Largest staged K/V copy the prefill allocates (4 GiB: 65536 tiles x KV heads).
+constexpr size_t kMaxKvxBytes = (size_t)4 << 30;
 
 int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc,
                               const float* ksc, const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off,
@@ -726,8 +728,16 @@ int rt4_attention_prefill_cfg(float* out, const uint32_t* qq, const float* qsc, 
     if (nsplit > 1 && ((rc = lib_scratch(kSlotAttnPart, rt4::fa_part_bytes(n_q, n_heads, nsplit), &part, st)) ||
                        (rc = lib_scratch(kSlotAttnCnt, rt4::fa_cnt_bytes(n_q, n_heads, nsplit), &cnt, st, true))))
         return rc;
+    // The staged K/V copy for the DMA form (one staging pass per call instead of per
+    // workgroup), up to kMaxKvxBytes; beyond that, or under capture while the copy
+    // would have to grow, each workgroup stages its own tiles (same results).
+    const size_t xb = rt4::fa_kvx_bytes(n_heads, ratio, n_tile);
+    void* kvx = nullptr;
+    if (xb <= kMaxKvxBytes && !(capturing(st) && !scratch_has(kSlotAttnKV, xb)) &&
+        (rc = lib_scratch(kSlotAttnKV, xb, &kvx, st)))
+        return rc;
     return hip_status(rt4::launch_fa_int4(out, qq, qsc, kc, ksc, vc, vsc, n_q, n_kv, off, n_tile, n_heads, ratio,
-                                          kv_cap, nsplit, static_cast<float*>(part), static_cast<int*>(cnt), st),
+                                          kv_cap, nsplit, static_cast<float*>(part), static_cast<int*>(cnt), kvx, st),
                       "k_attention launch");
 }
 

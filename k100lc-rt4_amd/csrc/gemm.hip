@@ -93,30 +93,6 @@ constexpr int LDS_BYTES = LDS_META + 48;
 constexpr int DMA_PER_UNIT = 5;   // DMA instructions per wave per unit
 constexpr int PART_FLOATS = NT * 64;   // one partial tile: 64 outputs per thread, [k][thread]
 
-__device__ __forceinline__ uint32_t lds_addr(const unsigned char* l) {
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(lds_void*)l);
-}
-// A wave-uniform pointer as a scalar register pair.
-__device__ __forceinline__ const void* sptr(const void* p) {
-    const uint64_t v = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-    return reinterpret_cast<const void*>((uintptr_t)(((uint64_t)hi << 32) | lo));
-}
-// global -> LDS: lane i's 16 (4) bytes at gbase + voff land at m0 + 16*i (4*i),
-// m0 = lbase + IMM.  The scalar base keeps the per-lane address a 32-bit offset.
-template <int IMM>
-__device__ __forceinline__ void dma16(uint32_t voff, const void* gbase, uint32_t lbase) {
-    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sptr(gbase)),
-                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
-                 : "memory");
-}
-template <int IMM>
-__device__ __forceinline__ void dma4(uint32_t voff, const void* gbase, uint32_t lbase) {
-    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sptr(gbase)),
-                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
-                 : "memory");
-}
 // Device-scope (sc1) 16-byte stores / loads of split-tile partials, the cache
 // policy of agent-scope atomics: the stores write through the per-XCD L2 and
 // are in memory once the writer's s_waitcnt has retired them, and the loads

@@ -82,4 +82,29 @@ __device__ __forceinline__ float load_dev(const float* p) {
     return v;
 }
 
+// LDS byte address of a pointer into shared memory (wave-uniform).
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* l) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)l);
+}
+// A wave-uniform pointer as a scalar register pair.
+__device__ __forceinline__ const void* sptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const void*>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
+// global -> LDS: lane i's 16 (4) bytes at gbase + voff land at m0 + 16*i (4*i),
+// m0 = lbase + IMM.  The scalar base keeps the per-lane address a 32-bit offset.
+template <int IMM>
+__device__ __forceinline__ void dma16(uint32_t voff, const void* gbase, uint32_t lbase) {
+    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sptr(gbase)),
+                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
+                 : "memory");
+}
+template <int IMM>
+__device__ __forceinline__ void dma4(uint32_t voff, const void* gbase, uint32_t lbase) {
+    asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sptr(gbase)),
+                 "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)lbase)), "n"(IMM)
+                 : "memory");
+}
 }  // namespace rt4

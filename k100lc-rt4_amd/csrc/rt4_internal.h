@@ -104,8 +104,13 @@ hipError_t launch_kv_append_v(uint32_t* vc, float* vsc, float* stage, const floa
 int fa_splits(int n_q, int n_heads, int n_tile, int cus);
 size_t fa_part_bytes(int n_q, int n_heads, int nsplit);
 size_t fa_cnt_bytes(int n_q, int n_heads, int nsplit);
+// Bytes of the staged K/V copy the DMA form of the prefill reads (two 16 KB blocks
+// per tile and KV head).  launch_fa_int4 with kvx (that many bytes) fills it and runs
+// the DMA form; with kvx null each workgroup stages its tiles itself.  Same results.
+size_t fa_kvx_bytes(int n_heads, int ratio, int n_tile);
 hipError_t launch_fa_int4(float* out, const uint32_t* qq, const float* qsc, const uint32_t* kc, const float* ksc,
                           const uint32_t* vc, const float* vsc, int n_q, int n_kv, int off, int n_tile,
-                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, hipStream_t st);
+                          int n_heads, int ratio, int kv_cap, int nsplit, float* part, int* cnt, void* kvx,
+                          hipStream_t st);
 
 }  // namespace rt4

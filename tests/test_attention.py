@@ -478,6 +478,45 @@ def test_attention_against_oracle(rt4, orc, torch_gpu, T, n_kv, off, H, KVH, cap
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T,n_kv,off,H,KVH,cap", [
+    (64, 64, 0, 2, 1, 64),                 # one tile
+    (128, 200, 72, 4, 2, 256),             # n_kv not a multiple of 64, kv_cap > n_kv
+    (128, 300, 172, 6, 2, 320),            # partial 8-key V group
+    (192, 1000, 808, 6, 1, 1024),          # GQA 6, partial last tile
+    (64, 520, 456, 8, 2, 576),             # GQA 4 over two KV heads
+])
+def test_attention_staged_copy_matches_in_kernel_staging(rt4, torch_gpu, T, n_kv, off, H, KVH, cap):
+    """The prefill stages K/V once per call into a copy that the workgroups DMA into
+    LDS.  Captured into a graph with no room for that copy (scratch released), every
+    workgroup stages its own tiles instead.  Both forms put the same operand bytes in
+    LDS, so the outputs must be bit-identical (one split: the automatic count also
+    falls back to one split under capture without workspace)."""
+    torch = torch_gpu
+    print(f"case staged copy vs in-kernel staging T={T} n_kv={n_kv} off={off} H={H} KVH={KVH} cap={cap}", flush=True)
+    rng = np.random.default_rng(29)
+    q, k, v = workload.attn_np(rng, T, n_kv, H, KVH)
+    TP = (T + 63) // 64 * 64
+    g = gpu_cache(rt4, torch, q, k, v, TP, cap)
+    kw = dict(n_kv=n_kv, off=off, ratio=H // KVH)
+    eager = host(rt4.attention_prefill(*g[:6], kv_splits=1, **kw))
+    for s in (1, 0):
+        torch.cuda.synchronize()
+        rt4.release_scratch()
+        out = torch.full((H, TP, HD), float("nan"), dtype=torch.float32, device="cuda")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            rt4.attention_prefill(*g[:6], kv_splits=s, out=out, **kw)
+        for _ in range(2):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(host(out).view(np.uint32), eager.view(np.uint32)), f"kv_splits={s}"
+        del graph
+        print(f"  captured kv_splits={s} (in-kernel staging) = eager (staged copy), bit for bit", flush=True)
+
+
+@pytest.mark.gpu
 def test_attention_benchmark_shape_sampled(rt4, orc, torch_gpu):
     """24 heads, GQA 6:1, 1024 queries over a 32768-token cache."""
     c4 = workload.ATTN_C4
