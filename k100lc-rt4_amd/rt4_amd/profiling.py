@@ -53,12 +53,14 @@ KERNELS = {                       # report key -> substring of the rocprof kerne
     "gemv_c0": "gemv_w4a8_dot_k<2, 5",
     "gemm_gate_up": "gemm_w4a8_k<false>",
     "attention_c4": "fa_int4_k",
+    "attention_c4_staging": "fa_expand_kv_k",
 }
 LABELS = {
     "gemv_gate_up": "gate/up GEMV (M=4, K=5120, N=17408)",
     "gemv_c0": "C0 GEMV (M=1, K=5120, N=5120)",
     "gemm_gate_up": "gate/up prefill GEMM (M=1024, K=5120, N=17408)",
     "attention_c4": "C4 attention (1024 queries over 33792 keys, 24/4 heads, D=256)",
+    "attention_c4_staging": "C4 attention K/V staging pass (once per call)",
 }
 
 
@@ -88,11 +90,19 @@ def attention_bytes(n_q: int, n_kv: int, H: int, KVH: int, D: int = 256) -> dict
     return parts
 
 
+def attention_staging_bytes(n_kv: int, KVH: int, D: int = 256) -> int:
+    """The prefill's K/V staging pass: the int4 K and V codes read once and their
+    staged operand bytes (16 KB per 64-key tile each for K and V) written once."""
+    n_tile = (n_kv + 63) // 64
+    return 2 * KVH * n_kv * D // 2 + 2 * KVH * n_tile * 16384
+
+
 ALGO_BYTES = {
     "gemv_gate_up": gemv_bytes(4, 17408, 5120),
     "gemv_c0": gemv_bytes(1, 5120, 5120),
     "gemm_gate_up": gemm_bytes(1024, 17408, 5120),
     "attention_c4": attention_bytes(1024, 32768 + 1024, 24, 4)["total"],
+    "attention_c4_staging": attention_staging_bytes(32768 + 1024, 4),
 }
 SIMDS_PER_CU = 4
 CUS_PER_XCD = 32
