@@ -95,6 +95,9 @@ __device__ __forceinline__ const void* sptr(const void* p) {
 }
 // global -> LDS: lane i's 16 (4) bytes at gbase + voff land at m0 + 16*i (4*i),
 // m0 = lbase + IMM.  The scalar base keeps the per-lane address a 32-bit offset.
+// m0 is a reserved register: the compiler holds no value in it across instructions
+// and sets it right before each instruction that reads it, so these writes need
+// no clobber (declaring one is refused with a warning).
 template <int IMM>
 __device__ __forceinline__ void dma16(uint32_t voff, const void* gbase, uint32_t lbase) {
     asm volatile("s_add_u32 m0, %2, %3\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sptr(gbase)),
