@@ -178,12 +178,12 @@ hipError_t launch_quant_row(int8_t* xq, float* sa, int32_t* asu, const float* x,
 // [rows][K], which is what the MFMA GEMM consumes.
 // GL = G/8 lanes per group.  grid (ceil(K/8/256), rows), block 256.
 template <int GL>
-__global__ __launch_bounds__(256) void quant_rows_a8_k(
+__global__ __launch_bounds__(512) void quant_rows_a8_k(
     const float* __restrict__ x, uint32_t* __restrict__ qh, uint32_t* __restrict__ ql,
     float* __restrict__ sc, float* __restrict__ sc16, int8_t* __restrict__ xq, int rows, int K,
     int in_stride, int in_off, int x_aligned) {
     const int r = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (K >> 3)) return;  // K%G==0: whole GL-lane runs exit together
     float v[8];
     load8(x + (size_t)r * in_stride + in_off + 8 * (size_t)i, x_aligned, v);
@@ -226,12 +226,12 @@ __global__ __launch_bounds__(256) void quant_rows_a8_k(
 // int4 activation quantizer (restates quant_rows_k, src/k_new.hip:192-219):
 // s = amax>0 ? amax/7 : 1, c = clamp(lrintf(x/s), -8, 7), nibble-packed, sc group-major.
 template <int GL>
-__global__ __launch_bounds__(256) void quant_rows_a4_k(const float* __restrict__ x,
+__global__ __launch_bounds__(512) void quant_rows_a4_k(const float* __restrict__ x,
                                                        uint32_t* __restrict__ q,
                                                        float* __restrict__ sc, int rows, int K,
                                                        int in_stride, int in_off, int x_aligned) {
     const int r = blockIdx.y;
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (K >> 3)) return;
     float v[8];
     load8(x + (size_t)r * in_stride + in_off + 8 * (size_t)i, x_aligned, v);
@@ -252,13 +252,13 @@ __global__ __launch_bounds__(256) void quant_rows_a4_k(const float* __restrict__
 
 #define RT4_GL_CASES(KERNEL, ...)                                                         \
     switch (G / 8) {                                                                      \
-        case 1: hipLaunchKernelGGL(KERNEL<1>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 2: hipLaunchKernelGGL(KERNEL<2>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 4: hipLaunchKernelGGL(KERNEL<4>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 8: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 16: hipLaunchKernelGGL(KERNEL<16>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 32: hipLaunchKernelGGL(KERNEL<32>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
-        case 64: hipLaunchKernelGGL(KERNEL<64>, grid, dim3(256), 0, st, __VA_ARGS__); break; \
+        case 1: hipLaunchKernelGGL(KERNEL<1>, grid, dim3(bs), 0, st, __VA_ARGS__); break;  \
+        case 2: hipLaunchKernelGGL(KERNEL<2>, grid, dim3(bs), 0, st, __VA_ARGS__); break;  \
+        case 4: hipLaunchKernelGGL(KERNEL<4>, grid, dim3(bs), 0, st, __VA_ARGS__); break;  \
+        case 8: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(bs), 0, st, __VA_ARGS__); break;  \
+        case 16: hipLaunchKernelGGL(KERNEL<16>, grid, dim3(bs), 0, st, __VA_ARGS__); break; \
+        case 32: hipLaunchKernelGGL(KERNEL<32>, grid, dim3(bs), 0, st, __VA_ARGS__); break; \
+        case 64: hipLaunchKernelGGL(KERNEL<64>, grid, dim3(bs), 0, st, __VA_ARGS__); break; \
         default: return hipErrorInvalidValue;                                             \
     }
 
@@ -266,11 +266,25 @@ bool quant_group_supported(int G) {
     return G >= 8 && G <= 512 && (G & (G - 1)) == 0;
 }
 
+// Lanes per workgroup for the row quantizers (one lane per 8 elements of a row,
+// one grid row per input row): the largest multiple of 64 up to 512 that divides
+// the K/8 lanes of a row, so that no workgroup is partly idle (K = 5120: 2 x 320
+// lanes instead of 256 + 256 + 128); 256 with a partial last workgroup when K/8 is
+// not a multiple of 64.  Multiples of 64 keep every G-group (at most 64 lanes)
+// inside one wave.
+int row_quant_lanes(int K) {
+    const int kd = K / 8;
+    for (int bs = 512; bs >= 64; bs -= 64)
+        if (kd % bs == 0) return bs;
+    return 256;
+}
+
 hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc16, int8_t* xq,
                                 const float* x, int rows, int K, int G, int in_stride, int in_off,
                                 hipStream_t st) {
     if (in_stride == 0) in_stride = K;
-    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int bs = row_quant_lanes(K);
+    const dim3 grid((K / 8 + bs - 1) / bs, rows);
     const int aligned = (((uintptr_t)(x + in_off)) & 15) == 0 && (in_stride % 4) == 0;
     RT4_GL_CASES(quant_rows_a8_k, x, qh, ql, sc, sc16, xq, rows, K, in_stride, in_off, aligned);
     return hipGetLastError();
@@ -279,7 +293,8 @@ hipError_t launch_quant_rows_a8(uint32_t* qh, uint32_t* ql, float* sc, float* sc
 hipError_t launch_quant_rows_a4(uint32_t* q, float* sc, const float* x, int rows, int K, int G,
                                 int in_stride, int in_off, hipStream_t st) {
     if (in_stride == 0) in_stride = K;
-    const dim3 grid((K / 8 + 255) / 256, rows);
+    const int bs = row_quant_lanes(K);
+    const dim3 grid((K / 8 + bs - 1) / bs, rows);
     const int aligned = (((uintptr_t)(x + in_off)) & 15) == 0 && (in_stride % 4) == 0;
     RT4_GL_CASES(quant_rows_a4_k, x, q, sc, rows, K, in_stride, in_off, aligned);
     return hipGetLastError();
