@@ -242,7 +242,7 @@ class GemmCase:
         self.M, self.N, self.K = M, N, K
         self.wq, ws = workload.weights_torch(N, K, generator=gen)
         self.sb = rt4_amd.make_group_major(ws, K)
-        x = workload.acts_torch(M, K, outliers=True, generator=gen)
+        self.x = x = workload.acts_torch(M, K, outliers=True, generator=gen)
         self.xq, self.sc = rt4_amd.quant_rows_i8(x)
         self.qh, self.ql, self.sc_, self.sc16 = rt4_amd.quant_rows_a8(x)
         self.aq4, self.sc4 = rt4_amd.quant_rows_a4(x)
@@ -258,12 +258,17 @@ class GemmCase:
     def w4a4(self, rt4_amd):
         rt4_amd.gemm_w4a4(self.wq, self.sb, self.aq4, self.sc4, out=self.c)
 
+    def quant(self, rt4_amd):
+        rt4_amd.quant_rows_a8(self.x)
+
 
 def gemm_entry(torch, rt4_amd, g: GemmCase, w4a4: bool = True) -> dict:
     """int8-MFMA TOPS = 2*M*N*K / kernel time (GEMM launch only, graph-replayed), plus
-    the whole drop-in k_gemm_i4_a8 call (digit recombination + GEMM)."""
+    the whole drop-in k_gemm_i4_a8 call (digit recombination + GEMM) and the drop-in
+    linear's activation quantizer k_quant_rows_a8 at this shape."""
     reps = 10
     runs = [("us", g.int8), ("dropin_us", g.dropin)] + ([("w4a4_dropin_us", g.w4a4)] if w4a4 else [])
+    runs.append(("quant_rows_a8_us", g.quant))
     for _, f in runs:                                          # eager first calls: kernel attributes
         f(rt4_amd)
     torch.cuda.synchronize()
