@@ -14,8 +14,10 @@ pytestmark = pytest.mark.gpu
 P = ctypes.c_void_p
 
 
+# workgroups of 320 / 128 / 128 / 256 / 64 / 256 (partial) / 448 / 192 lanes
 @pytest.mark.parametrize("rows,K,G", [(128, 5120, 128), (256, 17408, 128), (64, 1024, 64),
-                                      (32, 2048, 256), (8, 512, 512), (16, 256, 8)])
+                                      (32, 2048, 256), (8, 512, 512), (16, 256, 8), (16, 3584, 128),
+                                      (8, 4608, 64)])
 def test_quant_rows_a8_bit_exact(rt4, orc, torch_gpu, rows, K, G):
     print(f"case quant_rows_a8 rows={rows} K={K} G={G}", flush=True)
     x = workload.acts_np(np.random.default_rng(rows + K + G), rows, K, outliers=True)
@@ -92,7 +94,7 @@ def test_digits_to_i8_tail_and_unaligned(rt4, torch_gpu):
     assert np.array_equal(host(out_u), host(out))
 
 
-@pytest.mark.parametrize("rows,K,G", [(128, 5120, 128), (64, 512, 32)])
+@pytest.mark.parametrize("rows,K,G", [(128, 5120, 128), (64, 512, 32), (16, 3584, 128), (8, 384, 32)])
 def test_quant_rows_a4_bit_exact(rt4, orc, torch_gpu, rows, K, G):
     x = workload.acts_np(np.random.default_rng(7), rows, K)
     q, sc = rt4.quant_rows_a4(dev(torch_gpu, x), G=G)
